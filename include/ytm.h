@@ -1,0 +1,128 @@
+/*
+ * ytm.h -- C-ABI of libytm.so, the MI355X (gfx950) Tsetlin Machine hot path.
+ *
+ * This boundary replaces the reference's PyCUDA layer (src/cutm/base.py:128-206 compiles
+ * src/cutm/cuda/kernel.cu and drives its 9 kernels with prepared_call).  Every entry point
+ * below names the reference interface it stands in for.  Plain pointers and sizes only:
+ * host arrays are caller-owned and borrowed for the duration of a call; device memory is
+ * owned by the model / dataset handles.  Calls are synchronous on return, one HIP stream
+ * per model, not re-entrant per handle.  Every function returns 0 on success and a
+ * nonzero status otherwise; ytm_last_error() then describes the failure (thread-local).
+ */
+#ifndef YTM_H
+#define YTM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+enum {
+    YTM_OK = 0,
+    YTM_EINVAL = 1,   /* bad argument / unsupported configuration */
+    YTM_EHIP = 2,     /* HIP runtime error */
+    YTM_ETIMEOUT = 3, /* a persistent kernel's bounded wait expired */
+    YTM_ERANGE = 4    /* state value outside what the model can represent */
+};
+
+/* Model hyperparameters, resolved on the host exactly as src/cutm/base.py:60-121,129-152
+ * resolves them into #defines.  s_inv and q_prob are S_INV and Q_PROB as the reference's
+ * C preprocessor types them (float or double, kernel.cu:31-32), widened to double. */
+typedef struct ytm_params {
+    int32_t clauses;               /* CLAUSES = banks * number_of_clauses_per_class */
+    int32_t classes;               /* CLASSES */
+    int32_t dim0, dim1, dim2;      /* DIM0 (width), DIM1 (height), DIM2 (channels) */
+    int32_t patch_dim0, patch_dim1;/* PATCH_DIM0, PATCH_DIM1 */
+    int32_t number_of_ta_states;   /* MAX_TA_STATE */
+    int32_t max_included_literals; /* MAX_INCLUDED_LITERALS (resolved: LITERALS if None) */
+    int32_t append_negated;        /* APPEND_NEGATED */
+    int32_t encode_loc;            /* ENCODE_LOC */
+    int32_t coalesced;             /* COALESCED (CLAUSE_BANKS = coalesced ? 1 : CLASSES) */
+    int32_t negative_polarity;     /* NEGATIVE_CLAUSES */
+    int32_t init_neg_weights;      /* INIT_NEG_WEIGHTS */
+    int32_t thresh;                /* THRESH (T) */
+    double s_inv;                  /* S_INV */
+    double q_prob;                 /* Q_PROB */
+    uint64_t seed;                 /* key of the counter-based random stream */
+} ytm_params;
+
+typedef struct ytm_model ytm_model;
+typedef struct ytm_dataset ytm_dataset;
+
+/* Per-model counters and timings of the most recent calls (HIP events on the model's
+ * stream around the kernels named). */
+typedef struct ytm_stats {
+    uint64_t step;               /* samples trained so far (the random stream's step) */
+    uint64_t last_fit_samples;
+    uint64_t last_fit_updates;   /* (sample, clause) pairs that ran a Type Ia/Ib/II branch */
+    uint64_t total_updates;
+    double last_fit_kernel_ms;   /* sum over the training kernel launches of the last fit */
+    int32_t last_fit_launches;
+    int32_t train_workgroups;    /* persistent grid size used by the training kernel */
+    double last_score_kernel_ms; /* class-sum kernel of the last score */
+    double last_encode_kernel_ms;
+} ytm_stats;
+
+/* Thread-local description of the last failure. */
+const char *ytm_last_error(void);
+
+/* Model lifetime.  Replaces BaseTM._gpu_init / _reset_clauses / _reset_weights
+ * (src/cutm/base.py:128-222; kernel.cu:46-73 init_weights): TA states start at
+ * number_of_ta_states/2, weights from the INIT random site, patch weights and bias 0. */
+int ytm_create(const ytm_params *params, ytm_model **out);
+void ytm_destroy(ytm_model *m);
+/* L, W (=number_of_literal_chunks), P (=number_of_patches), number of TA bit-planes. */
+int ytm_geometry(const ytm_model *m, int64_t out[4]);
+int ytm_get_stats(const ytm_model *m, ytm_stats *out);
+/* Reseed the random stream and reset its step to 0 (what re-running __init__ does). */
+int ytm_set_seed(ytm_model *m, uint64_t seed);
+
+/* encode: BaseTM.encode (src/cutm/base.py:224-263; kernel.cu:76-152 encode_batch).
+ * X: uint32 (N, dim0*dim1*dim2), any value > 0 is a set pixel.  out: uint32 (N, P, W). */
+int ytm_encode(ytm_model *m, const uint32_t *X, int64_t N, uint32_t *out);
+
+/* Device-resident training / scoring data, so repeated epochs do not re-copy it.
+ * encX: uint32 (N, P, W); encY: int32 (N, classes) or NULL for score-only data. */
+int ytm_dataset_create(ytm_model *m, const uint32_t *encX, const int32_t *encY, int64_t N,
+                       ytm_dataset **out);
+void ytm_dataset_destroy(ytm_dataset *ds);
+
+/* fit: BaseTM._fit's per-sample loop (src/cutm/base.py:266-359; kernel.cu pack_clauses
+ * :155-204, fast_eval :255-282, select_active :285-316, clause_update :531-613).
+ * Samples [first, first+count) of ds, in order.  drop: uint32 (clauses) clause drop mask
+ * (base.py:288-293) or NULL for none.  inject: NULL for the counter-based stream, or a
+ * float buffer of count sample blocks [sel C*P | q C*K | upd C*K | lit C*K*L] replacing
+ * every draw (test mode).  Advances the model's step by count. */
+int ytm_fit_dataset(ytm_model *m, const ytm_dataset *ds, int64_t first, int64_t count,
+                    const uint32_t *drop, const float *inject);
+/* Host-array convenience form of the same (copies encX/encY in, like base.py:275-279). */
+int ytm_fit(ytm_model *m, const uint32_t *encX, const int32_t *encY, int64_t N,
+            const uint32_t *drop, const float *inject);
+
+/* score: BaseTM._score_batch (src/cutm/base.py:375-420; kernel.cu:319-343).
+ * class_sums: float (N, classes) = bias + sum of weights of non-empty firing clauses. */
+int ytm_score_dataset(ytm_model *m, const ytm_dataset *ds, float *class_sums);
+int ytm_score(ytm_model *m, const uint32_t *encX, int64_t N, float *class_sums);
+
+/* transform / transform_patchwise (src/cutm/base.py:465-542; kernel.cu:346-394).
+ * patchwise = 0: out uint32 (N, clauses); patchwise = 1: out uint32 (N, clauses, P). */
+int ytm_transform(ytm_model *m, const uint32_t *encX, int64_t N, int patchwise, uint32_t *out);
+
+/* State accessors (src/cutm/base.py:423-461, 561-593), flat C-order.
+ * ta_state: uint32 (clauses, L); weights: float (clauses, classes);
+ * patch_weights: int32 (clauses, P); bias: float (classes). */
+int ytm_get_ta_state(ytm_model *m, uint32_t *out);
+int ytm_set_ta_state(ytm_model *m, const uint32_t *in);
+int ytm_get_weights(ytm_model *m, float *out);
+int ytm_set_weights(ytm_model *m, const float *in);
+int ytm_get_patch_weights(ytm_model *m, int32_t *out);
+int ytm_set_patch_weights(ytm_model *m, const int32_t *in);
+int ytm_get_bias(ytm_model *m, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YTM_H */

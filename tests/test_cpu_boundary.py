@@ -1,0 +1,104 @@
+"""CPU-only checks of the drop-in boundary: libytm.so loads and exports every entry point
+include/ytm.h declares; the Python binding covers them; the reference's hyperparameter
+typing (base.py:129-152 pasted into kernel.cu:31-32) is reproduced."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    text = (ROOT / "include" / "ytm.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ytm_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_api():
+    names = declared_functions()
+    for required in ("ytm_create", "ytm_fit", "ytm_fit_dataset", "ytm_score", "ytm_encode", "ytm_transform",
+                     "ytm_get_ta_state", "ytm_set_ta_state", "ytm_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(ROOT / "ytm_amd" / "libytm.so"))
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_python_binding_covers_header():
+    from ytm_amd import _lib
+
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+
+
+def test_params_struct_layout():
+    """ytm_params in Python matches the C layout (int32 x 15, double x 2, uint64)."""
+    from ytm_amd._lib import YtmParams
+
+    assert ctypes.sizeof(YtmParams) == 15 * 4 + 4 + 8 + 8 + 8  # 4 bytes of padding before s_inv
+    assert YtmParams.s_inv.offset == 64 and YtmParams.seed.offset == 80
+
+
+def test_error_without_gpu_is_raised_not_swallowed():
+    import ytm_amd
+    from ytm_amd import _lib
+
+    try:
+        ytm_amd.MultiClassTM(10, 15, 3.9, (12, 1, 1), 2, seed=1)
+    except (ValueError, _lib.YtmError) as exc:  # no device here: libytm reports it
+        assert str(exc)
+    else:
+        pytest.skip("a GPU is visible; covered by the gpu tests")
+
+
+@pytest.mark.parametrize(
+    "s,expected",
+    [
+        (10, np.float32(1.0) / np.float32(10)),  # int literal: float division
+        (2, 0.5),
+        (10.0, 1.0 / 10.0),                      # floating literal: double division
+        (3.9, 1.0 / 3.9),
+        (np.float32(3.9), 1.0 / 3.9),             # pasted as the text "3.9"
+    ],
+)
+def test_s_inv_typing(s, expected, oracle_mod):
+    from ytm_amd.base import typed_s_inv
+
+    assert typed_s_inv(s) == float(expected)
+    assert oracle_mod.s_inv_of(s) == float(expected)
+
+
+def test_s_inv_int_is_not_double():
+    from ytm_amd.base import typed_s_inv
+
+    assert typed_s_inv(10) != 0.1  # 1.0f/10 is float(0.1) = 0.10000000149...
+    assert typed_s_inv(10.0) == 0.1
+
+
+@pytest.mark.parametrize(
+    "q,K,expected",
+    [
+        (1.0, 10, 1.0 / 9),                                  # default q (float) -> double
+        (1.0, 2, 1.0),                                       # max(1, K-1) = 1
+        (1.0, 1, 1.0),
+        (3, 10, float(np.float32(3.0) / np.float32(9))),   # int q -> float
+        (0.5, 3, 0.25),
+    ],
+)
+def test_q_prob_typing(q, K, expected, oracle_mod):
+    from ytm_amd.base import typed_q_prob
+
+    qq = min(q, float(K))  # base.py:81
+    assert typed_q_prob(qq, K) == expected
+    assert oracle_mod.q_prob_of(qq, K) == expected
+
+
+def test_q_is_min_of_q_and_classes():
+    # base.py:81 turns an int q >= K into float(K) (a double literal).
+    assert min(12, float(10)) == 10.0 and isinstance(min(12, float(10)), float)
+    assert isinstance(min(3, float(10)), int)

@@ -1,0 +1,261 @@
+"""HIP path (libytm.so on the GPU) against the C oracle, bit for bit.
+
+Parity bar: integer/bit work is bit-exact (encoded X, clause outputs, TA states, patch
+weights, update counts); class sums and weights are integer-valued floats and must be
+equal exactly as well.  Sizes are chosen so the oracle finishes in seconds; the full
+configurations are covered by size-independent properties at the end.
+"""
+import os
+import pickle
+
+import numpy as np
+import pytest
+
+import workloads
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+ytm_amd = pytest.importorskip("ytm_amd")
+from ytm_amd import MultiClassTM, MultiOutputTM  # noqa: E402
+
+orc.set_threads(min(16, os.cpu_count() or 1))
+
+
+def pair(cfg, n_train, n_test=0, clauses=None, seed=workloads.MODEL_SEED, **opts):
+    X, y, Xt, yt, kw = workloads.make(cfg, n_train, n_test)
+    if clauses is not None:
+        kw["number_of_clauses_per_class"] = clauses
+    kw.update(opts)
+    kw["seed"] = seed
+    print(f"[pair] cfg={cfg} n_train={n_train} kw={kw}", flush=True)
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(kw.pop("number_of_clauses_per_class"), kw.pop("T"), kw.pop("s"), kw.pop("dim"),
+                       kw.pop("n_classes"), **kw)
+    return tm, ref, X, y, Xt, yt
+
+
+def assert_state_equal(tm, ref, where=""):
+    np.testing.assert_array_equal(tm.get_ta_state().reshape(ref.ta.shape), ref.ta, err_msg=f"TA {where}")
+    np.testing.assert_array_equal(tm.get_weights().reshape(ref.w.shape), ref.w, err_msg=f"weights {where}")
+    np.testing.assert_array_equal(tm.get_patch_weights().reshape(ref.pw.shape), ref.pw, err_msg=f"pw {where}")
+
+
+# ------------------------------------------------------------------ encode / init
+@pytest.mark.parametrize("cfg,n", [(1, 64), (2, 32), (3, 8), (4, 4), (5, 16)])
+def test_encode(cfg, n):
+    tm, ref, X, *_ = pair(cfg, n)
+    np.testing.assert_array_equal(tm.encode(X), ref.encode(X))
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_initial_state(cfg):
+    tm, ref, *_ = pair(cfg, 1)
+    assert_state_equal(tm, ref, "init")
+    assert np.all(tm.get_literals() == 0)
+    assert np.all(tm.get_bias_weights() == 0)
+
+
+# ------------------------------------------------------------------ training
+@pytest.mark.parametrize(
+    "cfg,n,clauses,epochs",
+    [(1, 5000, None, 3), (2, 300, None, 2), (3, 40, None, 1), (3, 200, 200, 2), (4, 3, None, 1),
+     (4, 40, 500, 1), (5, 4, None, 1), (5, 60, 300, 2)],
+)
+def test_fit_counter_stream(cfg, n, clauses, epochs):
+    tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    for epoch in range(epochs):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, encY)
+        assert tm.stats()["last_fit_updates"] == upd, f"update count epoch {epoch}"
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+
+
+@pytest.mark.parametrize("cfg,n,clauses", [(1, 60, None), (2, 6, 40), (3, 5, 12), (4, 2, 6), (5, 3, 4)])
+def test_fit_injected_stream(cfg, n, clauses):
+    tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    rng = np.random.default_rng(cfg)
+    s_inv = np.float32(orc.s_inv_of(workloads.CONFIGS[cfg]["model"]["s"]))
+    for epoch in range(2):
+        inj = rng.random(tm.random_stream_size(n)).astype(np.float32)
+        inj[::13] = 1.0       # reservoir rejects u = 1.0
+        inj[7::29] = s_inv    # literal draw exactly at S_INV is accepted
+        tm.fit(encX, y, is_X_encoded=True, random_stream=inj)
+        upd = ref.fit_encoded(encX, encY, inject=inj)
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+
+
+@pytest.mark.parametrize(
+    "opts",
+    [dict(coalesced=False), dict(negative_polarity=False, init_neg_weights=False), dict(max_included_literals=4),
+     dict(append_negated=False), dict(number_of_ta_states=16), dict(q=3), dict(q=0.5)],
+)
+def test_fit_variant_flags(opts):
+    tm, ref, X, y, *_ = pair(2, 200, clauses=60, **opts)
+    encX = tm.encode(X)
+    for _ in range(2):
+        tm.fit(encX, y, is_X_encoded=True)
+        ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+    assert_state_equal(tm, ref, str(opts))
+
+
+def test_fit_conv_variant_no_loc():
+    tm, ref, X, y, *_ = pair(3, 30, clauses=50, encode_loc=False)
+    encX = tm.encode(X)
+    np.testing.assert_array_equal(encX, ref.encode(X))
+    tm.fit(encX, y, is_X_encoded=True)
+    ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+    assert_state_equal(tm, ref)
+
+
+def test_clause_drop():
+    tm, ref, X, y, *_ = pair(2, 150, clauses=80)
+    encX = tm.encode(X)
+    drop_rng = np.random.default_rng(workloads.MODEL_SEED)  # the model's numpy rng (base.py:123,289)
+    for _ in range(2):
+        tm.fit(encX, y, is_X_encoded=True, clause_drop_p=0.3)
+        drop = (drop_rng.random(ref.C) <= 0.3).astype(np.uint32)
+        ref.fit_encoded(encX, ref.encode_y_multiclass(y), drop=drop)
+    assert_state_equal(tm, ref)
+
+
+def test_launch_shape_independence(monkeypatch):
+    """The same seed gives the same model whatever the persistent grid / copy grouping."""
+    states = []
+    for wgs, group in [("", ""), ("3", "1"), ("17", "4"), ("256", "64")]:
+        monkeypatch.setenv("YTM_TRAIN_WGS", wgs)
+        monkeypatch.setenv("YTM_TRAIN_GROUP", group)
+        tm, _, X, y, *_ = pair(3, 60, clauses=100)
+        tm.fit(tm.encode(X), y, is_X_encoded=True)
+        states.append((tm.get_ta_state(), tm.get_weights(), tm.get_patch_weights()))
+    for s in states[1:]:
+        for a, b in zip(states[0], s):
+            np.testing.assert_array_equal(a, b)
+
+
+# ------------------------------------------------------------------ inference
+@pytest.mark.parametrize("cfg,n_train,n_test,clauses", [(1, 2000, 500, None), (2, 300, 300, None),
+                                                        (3, 60, 40, 300), (4, 10, 8, 400), (5, 40, 60, 300)])
+def test_score_transform(cfg, n_train, n_test, clauses):
+    tm, ref, X, y, Xt, yt = pair(cfg, n_train, n_test, clauses=clauses)
+    encX = tm.encode(X)
+    tm.fit(encX, y, is_X_encoded=True)
+    ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+    encXt = tm.encode(Xt)
+    preds, cs = tm.predict(encXt, is_X_encoded=True)
+    ref_cs = ref.score(encXt)
+    np.testing.assert_array_equal(cs, ref_cs)
+    np.testing.assert_array_equal(preds, np.argmax(ref_cs, axis=1))
+    np.testing.assert_array_equal(tm.transform(encXt, is_X_encoded=True), ref.transform(encXt))
+    n_pw = min(n_test, 12)
+    np.testing.assert_array_equal(tm.transform_patchwise(encXt[:n_pw], is_X_encoded=True),
+                                  ref.transform(encXt[:n_pw], patchwise=True))
+
+
+def test_score_edge_cases():
+    tm, ref, X, y, Xt, yt = pair(3, 30, 20, clauses=40)
+    # empty input
+    empty = np.zeros((0, tm.number_of_patches, tm.number_of_literal_chunks), dtype=np.uint32)
+    assert tm.score(empty, is_X_encoded=True).shape == (0, 10)
+    assert tm.transform(empty, is_X_encoded=True).shape == (0, tm.number_of_clauses)
+    # fresh model: every clause empty -> class sums are the (zero) bias, transform all ones
+    encXt = tm.encode(Xt)
+    np.testing.assert_array_equal(tm.score(encXt, is_X_encoded=True), np.zeros((20, 10), dtype=np.float32))
+    assert np.all(tm.transform(encXt, is_X_encoded=True) == 1)
+    # ragged tail: a batch that is not a multiple of any launch tile
+    tm.fit(tm.encode(X), y, is_X_encoded=True)
+    ref.fit_encoded(ref.encode(X), ref.encode_y_multiclass(y))
+    np.testing.assert_array_equal(tm.score(encXt[:7], is_X_encoded=True), ref.score(encXt[:7]))
+
+
+# ------------------------------------------------------------------ API surface
+def test_api_shapes_dtypes_errors():
+    tm, *_ = pair(3, 4, clauses=50)
+    X, y, Xt, yt, _ = workloads.make(3, 20, 10)
+    tm.fit(X, y)  # raw X path (encodes internally)
+    preds, cs = tm.predict(Xt)
+    assert preds.shape == (10,) and cs.shape == (10, 10) and cs.dtype == np.float32
+    assert tm.get_ta_state().shape == (50, 272) and tm.get_ta_state().dtype == np.uint32
+    assert tm.get_weights().shape == (50, 10) and tm.get_weights().dtype == np.float32
+    assert tm.get_patch_weights().shape == (50, 361) and tm.get_patch_weights().dtype == np.int32
+    assert tm.get_patch_weights().sum() > 0
+    with pytest.raises(AssertionError):
+        tm.encode(X.astype(np.int64))
+    with pytest.raises(AssertionError):
+        tm.fit(X, y.reshape(-1, 1))
+    with pytest.raises(OverflowError):
+        tm.transform_patchwise(_big_view(tm), is_X_encoded=True)
+
+
+def _big_view(tm):
+    # A zero-stride view with more samples than transform_patchwise accepts (no memory used).
+    n = np.iinfo(np.uint32).max // (tm.number_of_clauses * tm.number_of_patches) + 1
+    base = np.zeros((1, tm.number_of_patches, tm.number_of_literal_chunks), dtype=np.uint32)
+    return np.broadcast_to(base, (n,) + base.shape[1:])
+
+
+def test_non_coalesced_shapes():
+    X, y, *_ , kw = workloads.make(2, 50, 1)
+    kw.update(number_of_clauses_per_class=6, coalesced=False, seed=3)
+    tm = MultiClassTM(**kw)
+    tm.fit(X, y)
+    assert tm.get_ta_state().shape == (10, 6, 1568)
+    assert tm.get_weights().shape == (10, 6, 10)
+    w = tm.get_weights()
+    for bank in range(10):  # weights outside the own bank stay 0
+        assert np.all(np.delete(w[bank], bank, axis=1) == 0)
+
+
+def test_pickle_roundtrip():
+    tm, ref, X, y, Xt, yt = pair(2, 200, 50, clauses=50)
+    tm.fit(X, y)
+    blob = pickle.dumps(tm)
+    tm2 = pickle.loads(blob)
+    state = tm.__getstate__()
+    assert set(state) == {"args", "state"}
+    assert set(state["state"]) == {"ta_state", "clause_weights", "patch_weights", "min_y", "max_y"}
+    assert state["state"]["ta_state"].dtype == np.uint32 and state["state"]["ta_state"].ndim == 1
+    np.testing.assert_array_equal(tm2.get_ta_state(), tm.get_ta_state())
+    np.testing.assert_array_equal(tm2.get_weights(), tm.get_weights())
+    np.testing.assert_array_equal(tm2.predict(Xt)[1], tm.predict(Xt)[1])
+
+
+def test_multioutput():
+    X, y, Xt, yt, kw = workloads.make(2, 150, 40)
+    Y = np.stack([(y == k).astype(np.uint32) for k in range(10)], axis=1)
+    kw.update(number_of_clauses_per_class=60, seed=5)
+    tm = MultiOutputTM(**kw)
+    ref = orc.OracleTM(60, kw["T"], kw["s"], kw["dim"], 10, seed=5)
+    tm.fit(X, Y)
+    ref.fit_encoded(ref.encode(X), np.where(Y == 1, kw["T"], -kw["T"]).astype(np.int32))
+    assert_state_equal(tm, ref)
+    preds, cs = tm.predict(Xt)
+    np.testing.assert_array_equal(cs, ref.score(ref.encode(Xt)))
+    np.testing.assert_array_equal(preds, (cs >= 0).astype(np.uint32))
+
+
+# ------------------------------------------------------------------ full-size properties
+def test_full_config2_epoch_properties():
+    """Config 2 at its real size: one epoch in one call equals the same epoch in two calls
+    (step continuity across launches), the same seed reproduces it, and the states obey
+    0 <= s <= max(256, 128 + K)."""
+    X, y, Xt, yt, kw = workloads.make(2)
+    kw["seed"] = workloads.MODEL_SEED
+    a = MultiClassTM(**kw)
+    b = MultiClassTM(**kw)
+    encX = a.encode(X)
+    a.fit(encX, y, is_X_encoded=True)
+    b.fit(encX[:25000], y[:25000], is_X_encoded=True)
+    b.fit(encX[25000:], y[25000:], is_X_encoded=True)
+    ta = a.get_ta_state()
+    np.testing.assert_array_equal(ta, b.get_ta_state())
+    np.testing.assert_array_equal(a.get_weights(), b.get_weights())
+    assert ta.max() <= 256
+    acc = (a.predict(Xt)[0] == yt).mean()
+    print(f"config 2 after 1 epoch: test accuracy {acc:.4f}")
+    assert acc > 0.5

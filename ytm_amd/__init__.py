@@ -1,0 +1,8 @@
+"""ytm_amd -- MI355X-native Tsetlin Machine hot path with the cutm API of Mayur1009/YTM.
+
+    from ytm_amd import MultiClassTM   # instead of: from cutm import MultiClassTM
+"""
+from .multiclass import MultiClassTM as MultiClassTM
+from .multioutput import MultiOutputTM as MultiOutputTM
+
+__all__ = ["MultiClassTM", "MultiOutputTM"]

@@ -1,0 +1,554 @@
+// ytm_api.hip -- the extern "C" boundary of libytm.so (declared in include/ytm.h).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "ytm.h"
+#include "ytm_internal.h"
+
+using ytm::Geom;
+
+struct ytm_model {
+  ytm_params params;
+  Geom g;
+  int device = 0;
+  int cus = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  uint32_t* d_planes = nullptr;
+  float* d_w = nullptr;
+  int32_t* d_pw = nullptr;
+  float* d_bias = nullptr;
+  int32_t* d_ninc = nullptr;
+  float* d_inv_rank = nullptr;
+  unsigned long long* d_counters = nullptr;
+  int* d_err = nullptr;
+  unsigned long long* d_slots = nullptr;
+  size_t slots_bytes = 0;
+  ytm_stats stats;
+};
+
+struct ytm_dataset {
+  ytm_model* m;
+  uint32_t* d_X;
+  int32_t* d_Y;
+  int64_t N;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                            \
+  do {                                                                                           \
+    hipError_t e_ = (expr);                                                                      \
+    if (e_ != hipSuccess)                                                                        \
+      return fail(YTM_EHIP, std::string(#expr) + " failed: " + hipGetErrorString(e_));           \
+  } while (0)
+
+int ceil_log2(int64_t x) {
+  int b = 0;
+  while (((int64_t)1 << b) < x) ++b;
+  return b;
+}
+
+// Geometry of src/cutm/base.py:94-121 plus the bit-plane encoding of the TA states.
+int resolve_geometry(const ytm_params& p, Geom* out) {
+  Geom g{};
+  if (p.clauses < 1 || p.classes < 1) return fail(YTM_EINVAL, "clauses and classes must be >= 1");
+  if (p.classes > 64) return fail(YTM_EINVAL, "at most 64 classes are supported");
+  if (p.dim0 < 1 || p.dim1 < 1 || p.dim2 < 1) return fail(YTM_EINVAL, "dim entries must be >= 1");
+  if (p.patch_dim0 < 1 || p.patch_dim1 < 1 || p.patch_dim0 > p.dim0 || p.patch_dim1 > p.dim1)
+    return fail(YTM_EINVAL, "patch_dim must lie within dim");
+  if (p.number_of_ta_states < 1) return fail(YTM_EINVAL, "number_of_ta_states must be >= 1");
+  if (!p.coalesced && p.clauses % p.classes != 0)
+    return fail(YTM_EINVAL, "non-coalesced clause banks need clauses divisible by classes");
+  g.C = p.clauses;
+  g.K = p.classes;
+  g.dim0 = p.dim0; g.dim1 = p.dim1; g.dim2 = p.dim2;
+  g.pd0 = p.patch_dim0; g.pd1 = p.patch_dim1;
+  int64_t base = (int64_t)p.patch_dim0 * p.patch_dim1 * p.dim2;
+  if (p.encode_loc) base += (p.dim0 - p.patch_dim0) + (p.dim1 - p.patch_dim1);
+  g.Lh = base;
+  g.L = p.append_negated ? 2 * base : base;
+  g.W = (g.L - 1) / 32 + 1;
+  g.P = (int64_t)(p.dim0 - p.patch_dim0 + 1) * (p.dim1 - p.patch_dim1 + 1);
+  g.F = (int64_t)p.dim0 * p.dim1 * p.dim2;
+  if (g.P > 64 * 64) return fail(YTM_EINVAL, "at most 4096 patches are supported");
+  if (g.K * g.W * 6 >= ((int64_t)1 << 32)) return fail(YTM_EINVAL, "classes * literal words too large");
+  if (!p.encode_loc && g.P > 1) {
+    // kernel.cu:101-121 writes the thermometer bits even without ENCODE_LOC; the result is
+    // only defined while they stay inside the positive literals.
+    const int64_t top = std::max<int64_t>(p.dim1 - p.patch_dim1, (p.dim1 - p.patch_dim1) + (p.dim0 - p.patch_dim0));
+    if (top > g.Lh) return fail(YTM_EINVAL, "encode_loc=False with these patches writes outside the literals");
+  }
+  g.max_state = p.number_of_ta_states;
+  g.half_state = p.number_of_ta_states / 2;
+  const int64_t maxs = std::max<int64_t>(g.max_state, (int64_t)g.half_state + g.K);
+  const int top = std::max(1, std::max(ceil_log2((int64_t)g.half_state + 1), ceil_log2(maxs - g.half_state)));
+  g.np = top + 1;
+  if (g.np > ytm::kMaxPlanesHost) return fail(YTM_EINVAL, "number_of_ta_states too large for the bit-plane state");
+  g.off = (uint32_t)(((int64_t)1 << top) - g.half_state - 1);
+  g.max_state_p = (uint32_t)g.max_state + g.off;
+  g.last_filter = (g.L % 32) ? ~(0xFFFFFFFFu << (g.L % 32)) : 0xFFFFFFFFu;
+  g.per_bank = (int)(p.coalesced ? g.C : g.C / g.K);
+  g.append_negated = p.append_negated;
+  g.encode_loc = p.encode_loc;
+  g.coalesced = p.coalesced;
+  g.negative_polarity = p.negative_polarity;
+  g.init_neg_weights = p.init_neg_weights;
+  g.maxinc = p.max_included_literals;
+  g.thresh = (double)p.thresh;
+  g.s_inv = p.s_inv;
+  g.q_prob = p.q_prob;
+  // u <= s_inv with u = (q + 1) * 2^-24  <=>  q < floor(s_inv * 2^24).
+  const double scaled = std::floor(p.s_inv * 16777216.0);
+  g.s_thr = !(scaled > 0.0) ? 0u : (scaled >= 16777216.0 ? (1u << 24) : (uint32_t)scaled);
+  *out = g;
+  return YTM_OK;
+}
+
+int ensure_slots(ytm_model* m, size_t bytes) {
+  if (m->slots_bytes >= bytes) return YTM_OK;
+  if (m->d_slots) HIP_TRY(hipFree(m->d_slots));
+  m->d_slots = nullptr;
+  m->slots_bytes = 0;
+  HIP_TRY(hipMalloc(&m->d_slots, bytes));
+  m->slots_bytes = bytes;
+  return YTM_OK;
+}
+
+int upload(void** dst, const void* src, size_t bytes, hipStream_t s) {
+  HIP_TRY(hipMalloc(dst, bytes > 0 ? bytes : 4));
+  if (bytes) HIP_TRY(hipMemcpyAsync(*dst, src, bytes, hipMemcpyHostToDevice, s));
+  return YTM_OK;
+}
+
+// Picks the persistent grid: one workgroup per CU at most, at least ~8 clauses each.
+void train_shape(const ytm_model* m, int* grid, int* D, int* cpw) {
+  const char* env = std::getenv("YTM_TRAIN_WGS");
+  int64_t G = std::min<int64_t>(m->cus, std::max<int64_t>(1, (m->g.C + 7) / 8));
+  if (env && std::atoi(env) > 0) G = std::min<int64_t>(std::atoi(env), m->g.C);
+  *grid = (int)G;
+  const char* envd = std::getenv("YTM_TRAIN_GROUP");
+  int per_copy = envd && std::atoi(envd) > 0 ? std::atoi(envd) : 16;
+  *D = (int)((G + per_copy - 1) / per_copy);
+  *cpw = (int)((m->g.C + G - 1) / G) + 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ytm_last_error(void) { return g_error.c_str(); }
+
+int ytm_create(const ytm_params* params, ytm_model** out) {
+  if (!params || !out) return fail(YTM_EINVAL, "null argument");
+  *out = nullptr;
+  Geom g;
+  int rc = resolve_geometry(*params, &g);
+  if (rc) return rc;
+  ytm_model* m = new ytm_model();
+  m->params = *params;
+  m->g = g;
+  std::memset(&m->stats, 0, sizeof(m->stats));
+  auto cleanup = [&](int code) {
+    ytm_destroy(m);
+    return code;
+  };
+  if (hipGetDevice(&m->device) != hipSuccess) return cleanup(fail(YTM_EHIP, "no HIP device"));
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, m->device) != hipSuccess) return cleanup(fail(YTM_EHIP, "device query failed"));
+  m->cus = prop.multiProcessorCount;
+  if (!prop.cooperativeLaunch) return cleanup(fail(YTM_EHIP, "device lacks cooperative launch"));
+#define CREATE_TRY(expr)                                                                       \
+  do {                                                                                         \
+    hipError_t e_ = (expr);                                                                    \
+    if (e_ != hipSuccess)                                                                      \
+      return cleanup(fail(YTM_EHIP, std::string(#expr) + " failed: " + hipGetErrorString(e_))); \
+  } while (0)
+  CREATE_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+  CREATE_TRY(hipEventCreate(&m->ev0));
+  CREATE_TRY(hipEventCreate(&m->ev1));
+  CREATE_TRY(hipMalloc(&m->d_planes, (size_t)(g.C * g.np * g.W) * 4));
+  CREATE_TRY(hipMalloc(&m->d_w, (size_t)(g.C * g.K) * 4));
+  CREATE_TRY(hipMalloc(&m->d_pw, (size_t)(g.C * g.P) * 4));
+  CREATE_TRY(hipMalloc(&m->d_bias, (size_t)g.K * 4));
+  CREATE_TRY(hipMalloc(&m->d_ninc, (size_t)g.C * 4));
+  CREATE_TRY(hipMalloc(&m->d_inv_rank, (size_t)(g.P + 1) * 4));
+  CREATE_TRY(hipMalloc(&m->d_counters, 64));
+  CREATE_TRY(hipMalloc(&m->d_err, 4));
+  std::vector<float> inv((size_t)g.P + 1);
+  inv[0] = 0.0f;
+  for (int64_t r = 1; r <= g.P; ++r) inv[r] = 1.0f / (float)r;  // IEEE fp32 division
+  CREATE_TRY(hipMemcpyAsync(m->d_inv_rank, inv.data(), inv.size() * 4, hipMemcpyHostToDevice, m->stream));
+  CREATE_TRY(hipMemsetAsync(m->d_pw, 0, (size_t)(g.C * g.P) * 4, m->stream));
+  CREATE_TRY(hipMemsetAsync(m->d_bias, 0, (size_t)g.K * 4, m->stream));
+  CREATE_TRY(ytm::launch_init_state(m->d_planes, m->d_w, g, params->seed, m->stream));
+  CREATE_TRY(hipStreamSynchronize(m->stream));
+#undef CREATE_TRY
+  *out = m;
+  return YTM_OK;
+}
+
+void ytm_destroy(ytm_model* m) {
+  if (!m) return;
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  void* bufs[] = {m->d_planes, m->d_w, m->d_pw, m->d_bias, m->d_ninc, m->d_inv_rank, m->d_counters, m->d_err, m->d_slots};
+  for (void* b : bufs)
+    if (b) (void)hipFree(b);
+  if (m->ev0) (void)hipEventDestroy(m->ev0);
+  if (m->ev1) (void)hipEventDestroy(m->ev1);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+int ytm_geometry(const ytm_model* m, int64_t out[4]) {
+  if (!m || !out) return fail(YTM_EINVAL, "null argument");
+  out[0] = m->g.L;
+  out[1] = m->g.W;
+  out[2] = m->g.P;
+  out[3] = m->g.np;
+  return YTM_OK;
+}
+
+int ytm_get_stats(const ytm_model* m, ytm_stats* out) {
+  if (!m || !out) return fail(YTM_EINVAL, "null argument");
+  *out = m->stats;
+  return YTM_OK;
+}
+
+int ytm_set_seed(ytm_model* m, uint64_t seed) {
+  if (!m) return fail(YTM_EINVAL, "null argument");
+  m->params.seed = seed;
+  m->stats.step = 0;
+  return YTM_OK;
+}
+
+int ytm_encode(ytm_model* m, const uint32_t* X, int64_t N, uint32_t* out) {
+  if (!m || (N > 0 && (!X || !out)) || N < 0) return fail(YTM_EINVAL, "bad encode arguments");
+  if (N == 0) return YTM_OK;
+  const Geom& g = m->g;
+  // Chunk so that one chunk's encoded output stays below 1 GiB.
+  const int64_t per = std::max<int64_t>(1, ((int64_t)1 << 30) / (g.P * g.W * 4));
+  uint32_t *dX = nullptr, *dO = nullptr;
+  const int64_t chunk = std::min(per, N);
+  HIP_TRY(hipMalloc(&dX, (size_t)(chunk * g.F) * 4));
+  hipError_t e = hipMalloc(&dO, (size_t)(chunk * g.P * g.W) * 4);
+  if (e != hipSuccess) {
+    (void)hipFree(dX);
+    return fail(YTM_EHIP, std::string("hipMalloc failed: ") + hipGetErrorString(e));
+  }
+  double ms_total = 0.0;
+  int rc = YTM_OK;
+  for (int64_t s = 0; s < N && rc == YTM_OK; s += chunk) {
+    const int64_t n = std::min(chunk, N - s);
+    e = hipMemcpyAsync(dX, X + s * g.F, (size_t)(n * g.F) * 4, hipMemcpyHostToDevice, m->stream);
+    if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
+    if (e == hipSuccess) e = ytm::launch_encode(dX, n, dO, g, m->stream);
+    if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(out + s * g.P * g.W, dO, (size_t)(n * g.P * g.W) * 4, hipMemcpyDeviceToHost, m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, m->ev0, m->ev1);
+    ms_total += ms;
+    if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("encode failed: ") + hipGetErrorString(e));
+  }
+  m->stats.last_encode_kernel_ms = ms_total;
+  (void)hipFree(dX);
+  (void)hipFree(dO);
+  return rc;
+}
+
+int ytm_dataset_create(ytm_model* m, const uint32_t* encX, const int32_t* encY, int64_t N, ytm_dataset** out) {
+  if (!m || !out || N < 0 || (N > 0 && !encX)) return fail(YTM_EINVAL, "bad dataset arguments");
+  *out = nullptr;
+  const Geom& g = m->g;
+  ytm_dataset* ds = new ytm_dataset{m, nullptr, nullptr, N};
+  int rc = upload((void**)&ds->d_X, encX, (size_t)(N * g.P * g.W) * 4, m->stream);
+  if (!rc && encY) rc = upload((void**)&ds->d_Y, encY, (size_t)(N * g.K) * 4, m->stream);
+  if (!rc) {
+    hipError_t e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) rc = fail(YTM_EHIP, hipGetErrorString(e));
+  }
+  if (rc) {
+    ytm_dataset_destroy(ds);
+    return rc;
+  }
+  *out = ds;
+  return YTM_OK;
+}
+
+void ytm_dataset_destroy(ytm_dataset* ds) {
+  if (!ds) return;
+  if (ds->d_X) (void)hipFree(ds->d_X);
+  if (ds->d_Y) (void)hipFree(ds->d_Y);
+  delete ds;
+}
+
+int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count, const uint32_t* drop,
+                    const float* inject) {
+  if (!m || !ds || ds->m != m) return fail(YTM_EINVAL, "dataset does not belong to this model");
+  if (!ds->d_Y) return fail(YTM_EINVAL, "dataset has no targets");
+  if (first < 0 || count < 0 || first + count > ds->N) return fail(YTM_EINVAL, "sample range out of bounds");
+  m->stats.last_fit_samples = 0;
+  m->stats.last_fit_updates = 0;
+  m->stats.last_fit_kernel_ms = 0.0;
+  m->stats.last_fit_launches = 0;
+  if (count == 0) return YTM_OK;
+  const Geom& g = m->g;
+  int grid, D, cpw;
+  train_shape(m, &grid, &D, &cpw);
+  const size_t lds = ytm::train_lds_bytes(cpw, D, (int)g.K);
+  const bool vanilla = g.P == 1;
+  const bool inj = inject != nullptr;
+  int bpc = 0;
+  HIP_TRY(ytm::train_occupancy(vanilla, inj, lds, &bpc));
+  if ((int64_t)bpc * m->cus < grid)
+    return fail(YTM_EINVAL, "training grid does not fit co-resident on the device");
+  m->stats.train_workgroups = grid;
+
+  // Per-launch sample count: bounded by the class-sum slot memory (<= 256 MiB) and, in
+  // injected mode, by the size of the injected block buffer (<= 1 GiB).
+  const int64_t slot_row = (int64_t)D * g.K * 8;
+  int64_t per_launch = std::max<int64_t>(1, ((int64_t)256 << 20) / slot_row);
+  const int64_t block = g.C * g.P + 2 * g.C * g.K + g.C * g.K * g.L;
+  if (inj) per_launch = std::min<int64_t>(per_launch, std::max<int64_t>(1, ((int64_t)1 << 30) / (block * 4)));
+  per_launch = std::min<int64_t>(per_launch, count);
+  int rc = ensure_slots(m, (size_t)(per_launch * slot_row));
+  if (rc) return rc;
+
+  uint32_t* d_drop = nullptr;
+  float* d_inj = nullptr;
+  std::vector<uint32_t> zeros;
+  if (!drop) {
+    zeros.assign((size_t)g.C, 0u);
+    drop = zeros.data();
+  }
+  rc = upload((void**)&d_drop, drop, (size_t)g.C * 4, m->stream);
+  if (rc) return rc;
+  if (inj) {
+    hipError_t e = hipMalloc(&d_inj, (size_t)(per_launch * block) * 4);
+    if (e != hipSuccess) {
+      (void)hipFree(d_drop);
+      return fail(YTM_EHIP, std::string("hipMalloc(inject) failed: ") + hipGetErrorString(e));
+    }
+  }
+  auto finish = [&](int code) {
+    (void)hipStreamSynchronize(m->stream);
+    if (d_drop) (void)hipFree(d_drop);
+    if (d_inj) (void)hipFree(d_inj);
+    return code;
+  };
+#define FIT_TRY(expr)                                                                           \
+  do {                                                                                          \
+    hipError_t e_ = (expr);                                                                     \
+    if (e_ != hipSuccess)                                                                       \
+      return finish(fail(YTM_EHIP, std::string(#expr) + " failed: " + hipGetErrorString(e_)));  \
+  } while (0)
+
+  FIT_TRY(hipMemsetAsync(m->d_counters, 0, 64, m->stream));
+  FIT_TRY(hipMemsetAsync(m->d_err, 0, 4, m->stream));
+  double ms_total = 0.0;
+  int launches = 0;
+  for (int64_t s = 0; s < count; s += per_launch) {
+    const int64_t n = std::min(per_launch, count - s);
+    if (inj)
+      FIT_TRY(hipMemcpyAsync(d_inj, inject + s * block, (size_t)(n * block) * 4, hipMemcpyHostToDevice, m->stream));
+    FIT_TRY(ytm::launch_fill_u64(m->d_slots, n * D * g.K, m->stream));
+    ytm::TrainArgs a{};
+    a.planes = m->d_planes;
+    a.weights = m->d_w;
+    a.patch_w = m->d_pw;
+    a.bias = m->d_bias;
+    a.X = ds->d_X + (first + s) * g.P * g.W;
+    a.Y = ds->d_Y + (first + s) * g.K;
+    a.drop = d_drop;
+    a.inject = d_inj;
+    a.inv_rank = m->d_inv_rank;
+    a.slots = m->d_slots;
+    a.counters = m->d_counters;
+    a.err = m->d_err;
+    a.inject_block = block;
+    a.step0 = m->stats.step + (uint64_t)s;
+    a.seed = m->params.seed;
+    a.N = (int)n;
+    a.D = D;
+    a.cpw = cpw;
+    a.g = g;
+    FIT_TRY(hipEventRecord(m->ev0, m->stream));
+    FIT_TRY(ytm::launch_train(a, grid, lds, vanilla, inj, m->stream));
+    FIT_TRY(hipEventRecord(m->ev1, m->stream));
+    FIT_TRY(hipEventSynchronize(m->ev1));
+    float ms = 0.0f;
+    FIT_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+    ms_total += ms;
+    ++launches;
+    int herr = 0;
+    FIT_TRY(hipMemcpy(&herr, m->d_err, 4, hipMemcpyDeviceToHost));
+    if (herr) return finish(fail(YTM_ETIMEOUT, "training kernel: a workgroup's bounded wait for the class sums expired"));
+  }
+  unsigned long long upd = 0;
+  FIT_TRY(hipMemcpy(&upd, m->d_counters, 8, hipMemcpyDeviceToHost));
+#undef FIT_TRY
+  m->stats.step += (uint64_t)count;
+  m->stats.last_fit_samples = (uint64_t)count;
+  m->stats.last_fit_updates = upd;
+  m->stats.total_updates += upd;
+  m->stats.last_fit_kernel_ms = ms_total;
+  m->stats.last_fit_launches = launches;
+  return finish(YTM_OK);
+}
+
+int ytm_fit(ytm_model* m, const uint32_t* encX, const int32_t* encY, int64_t N, const uint32_t* drop,
+            const float* inject) {
+  if (!m || N < 0 || (N > 0 && (!encX || !encY))) return fail(YTM_EINVAL, "bad fit arguments");
+  ytm_dataset* ds = nullptr;
+  int rc = ytm_dataset_create(m, encX, encY, N, &ds);
+  if (rc) return rc;
+  rc = ytm_fit_dataset(m, ds, 0, N, drop, inject);
+  ytm_dataset_destroy(ds);
+  return rc;
+}
+
+int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
+  if (!m || !ds || ds->m != m || (ds->N > 0 && !class_sums)) return fail(YTM_EINVAL, "bad score arguments");
+  const Geom& g = m->g;
+  const int64_t N = ds->N;
+  if (N == 0) return YTM_OK;
+  long long* acc = nullptr;
+  float* dout = nullptr;
+  HIP_TRY(hipMalloc(&acc, (size_t)(N * g.K) * 8));
+  hipError_t e = hipMalloc(&dout, (size_t)(N * g.K) * 4);
+  int rc = YTM_OK;
+  if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
+  if (e == hipSuccess) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
+  if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
+  if (e == hipSuccess) e = ytm::launch_score(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->stream);
+  if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
+  if (e == hipSuccess) e = ytm::launch_score_finish(acc, m->d_bias, N, g, dout, m->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(class_sums, dout, (size_t)(N * g.K) * 4, hipMemcpyDeviceToHost, m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, m->ev0, m->ev1);
+  if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("score failed: ") + hipGetErrorString(e));
+  m->stats.last_score_kernel_ms = ms;
+  if (acc) (void)hipFree(acc);
+  if (dout) (void)hipFree(dout);
+  return rc;
+}
+
+int ytm_score(ytm_model* m, const uint32_t* encX, int64_t N, float* class_sums) {
+  if (!m || N < 0 || (N > 0 && (!encX || !class_sums))) return fail(YTM_EINVAL, "bad score arguments");
+  ytm_dataset* ds = nullptr;
+  int rc = ytm_dataset_create(m, encX, nullptr, N, &ds);
+  if (rc) return rc;
+  rc = ytm_score_dataset(m, ds, class_sums);
+  ytm_dataset_destroy(ds);
+  return rc;
+}
+
+int ytm_transform(ytm_model* m, const uint32_t* encX, int64_t N, int patchwise, uint32_t* out) {
+  if (!m || N < 0 || (N > 0 && (!encX || !out))) return fail(YTM_EINVAL, "bad transform arguments");
+  if (N == 0) return YTM_OK;
+  const Geom& g = m->g;
+  const size_t out_n = (size_t)(N * g.C * (patchwise ? g.P : 1));
+  uint32_t *dX = nullptr, *dO = nullptr;
+  int rc = upload((void**)&dX, encX, (size_t)(N * g.P * g.W) * 4, m->stream);
+  if (rc) return rc;
+  hipError_t e = hipMalloc(&dO, out_n * 4);
+  if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
+  if (e == hipSuccess) e = ytm::launch_transform(m->d_planes, m->d_ninc, dX, N, g, patchwise, dO, m->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out, dO, out_n * 4, hipMemcpyDeviceToHost, m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("transform failed: ") + hipGetErrorString(e));
+  (void)hipFree(dX);
+  if (dO) (void)hipFree(dO);
+  return rc;
+}
+
+int ytm_get_ta_state(ytm_model* m, uint32_t* out) {
+  if (!m || !out) return fail(YTM_EINVAL, "null argument");
+  const Geom& g = m->g;
+  uint32_t* d = nullptr;
+  HIP_TRY(hipMalloc(&d, (size_t)(g.C * g.L) * 4));
+  hipError_t e = ytm::launch_planes_to_ta(m->d_planes, d, g, m->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out, d, (size_t)(g.C * g.L) * 4, hipMemcpyDeviceToHost, m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(YTM_EHIP, std::string("get_ta_state failed: ") + hipGetErrorString(e));
+  return YTM_OK;
+}
+
+int ytm_set_ta_state(ytm_model* m, const uint32_t* in) {
+  if (!m || !in) return fail(YTM_EINVAL, "null argument");
+  const Geom& g = m->g;
+  // Representable and closed under the feedback dynamics: s' = s + off < 2^np.
+  const uint64_t limit = ((uint64_t)1 << g.np) - 1 - g.off;
+  for (int64_t i = 0; i < g.C * g.L; ++i)
+    if ((uint64_t)in[i] > limit)
+      return fail(YTM_ERANGE, "TA state " + std::to_string(in[i]) + " exceeds the representable maximum " +
+                                  std::to_string(limit));
+  uint32_t* d = nullptr;
+  int rc = upload((void**)&d, in, (size_t)(g.C * g.L) * 4, m->stream);
+  if (rc) return rc;
+  hipError_t e = ytm::launch_ta_to_planes(d, m->d_planes, g, m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(YTM_EHIP, std::string("set_ta_state failed: ") + hipGetErrorString(e));
+  return YTM_OK;
+}
+
+int ytm_get_weights(ytm_model* m, float* out) {
+  if (!m || !out) return fail(YTM_EINVAL, "null argument");
+  HIP_TRY(hipMemcpyAsync(out, m->d_w, (size_t)(m->g.C * m->g.K) * 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  return YTM_OK;
+}
+
+int ytm_set_weights(ytm_model* m, const float* in) {
+  if (!m || !in) return fail(YTM_EINVAL, "null argument");
+  for (int64_t i = 0; i < m->g.C * m->g.K; ++i) {
+    const float v = in[i];
+    if (!(std::fabs(v) < 2147483648.0f) || std::nearbyint(v) != v)
+      return fail(YTM_ERANGE, "clause weights must be integer-valued floats below 2^31 in magnitude");
+  }
+  HIP_TRY(hipMemcpyAsync(m->d_w, in, (size_t)(m->g.C * m->g.K) * 4, hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  return YTM_OK;
+}
+
+int ytm_get_patch_weights(ytm_model* m, int32_t* out) {
+  if (!m || !out) return fail(YTM_EINVAL, "null argument");
+  HIP_TRY(hipMemcpyAsync(out, m->d_pw, (size_t)(m->g.C * m->g.P) * 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  return YTM_OK;
+}
+
+int ytm_set_patch_weights(ytm_model* m, const int32_t* in) {
+  if (!m || !in) return fail(YTM_EINVAL, "null argument");
+  HIP_TRY(hipMemcpyAsync(m->d_pw, in, (size_t)(m->g.C * m->g.P) * 4, hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  return YTM_OK;
+}
+
+int ytm_get_bias(ytm_model* m, float* out) {
+  if (!m || !out) return fail(YTM_EINVAL, "null argument");
+  HIP_TRY(hipMemcpyAsync(out, m->d_bias, (size_t)m->g.K * 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  return YTM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,728 @@
+// ytm_kernels.hip -- hand-written gfx950 kernels of the YTM Tsetlin Machine hot path.
+//
+// Data layout in HBM (per model):
+//   planes  uint32 [C][np][W]   bit-sliced TA states; plane np-1 is the include mask
+//   weights float  [C][K]       clause weights (integer-valued, as the reference keeps them)
+//   patch_w int32  [C][P]       reservoir selection counts
+// Encoded inputs keep the reference layout uint32 [N][P][W] (src/cutm/base.py:238).
+#include "ytm_device.h"
+#include "ytm_internal.h"
+
+namespace ytm {
+
+// ============================================================================ encode
+// One thread per output word (e, p, w); every bit is the closed form of what
+// encode_batch (src/cutm/cuda/kernel.cu:76-152) leaves in that bit:
+//   negated literal l+L/2 = NOT positive literal l (the prefilled negated half is cleared
+//   exactly where a positive bit is set); positives are the y/x thermometers and the
+//   patch pixels; bits >= L stay 0 (the reference memsets the output first).
+__device__ __forceinline__ uint32_t positive_literal(const uint32_t* Xe, const Geom& g, int64_t li,
+                                                     int64_t py, int64_t px) {
+  const int64_t ty = g.dim1 - g.pd1, tx = g.dim0 - g.pd0;
+  int64_t idx = li;
+  bool therm = false;
+  if (g.encode_loc) {
+    if (li < ty) return li < py ? 1u : 0u;
+    if (li < ty + tx) return (li - ty) < px ? 1u : 0u;
+    idx = li - ty - tx;
+  } else {
+    // The thermometer loops of kernel.cu:101-121 run even without ENCODE_LOC and write
+    // over the first pixel literals; reproduced as-is.
+    therm = (li < py) || (li >= ty && li < ty + px);
+  }
+  const int64_t row = (int64_t)g.pd0 * g.dim2;
+  const int64_t ry = idx / row, rem = idx % row;
+  const int64_t rx = rem / g.dim2, z = rem % g.dim2;
+  const uint32_t v = Xe[(py + ry) * ((int64_t)g.dim0 * g.dim2) + (px + rx) * g.dim2 + z];
+  return (v > 0u || therm) ? 1u : 0u;
+}
+
+__global__ __launch_bounds__(256) void encode_kernel(const uint32_t* __restrict__ X, int64_t N,
+                                                     uint32_t* __restrict__ out, Geom g) {
+  const int64_t total = N * g.P * g.W;
+  const int64_t xw = g.dim0 - g.pd0 + 1;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t w = idx % g.W;
+    const int64_t ep = idx / g.W;
+    const int64_t p = ep % g.P, e = ep / g.P;
+    const int64_t py = p / xw, px = p % xw;
+    const uint32_t* Xe = X + e * g.F;
+    uint32_t word = 0u;
+    for (int b = 0; b < 32; ++b) {
+      const int64_t l = w * 32 + b;
+      if (l >= g.L) break;
+      uint32_t bit;
+      if (g.append_negated && l >= g.Lh)
+        bit = positive_literal(Xe, g, l - g.Lh, py, px) ^ 1u;
+      else
+        bit = positive_literal(Xe, g, l, py, px);
+      word |= bit << b;
+    }
+    out[idx] = word;
+  }
+}
+
+// ===================================================================== TA state I/O
+// uint32 (C, L) states <-> bit-planes.  Literals >= L of the last word hold s = 0 and are
+// never updated or included.
+__global__ __launch_bounds__(256) void ta_to_planes_kernel(const uint32_t* __restrict__ ta,
+                                                           uint32_t* __restrict__ planes, Geom g) {
+  const int64_t total = g.C * g.W;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t c = idx / g.W, w = idx % g.W;
+    uint32_t pl[kMaxPlanes];
+#pragma unroll
+    for (int j = 0; j < kMaxPlanes; ++j) pl[j] = 0u;
+    for (int b = 0; b < 32; ++b) {
+      const int64_t l = w * 32 + b;
+      const uint32_t s = (l < g.L ? ta[c * g.L + l] : 0u) + g.off;
+#pragma unroll
+      for (int j = 0; j < kMaxPlanes; ++j) pl[j] |= ((s >> j) & 1u) << b;
+    }
+    for (int j = 0; j < g.np; ++j) planes[(c * g.np + j) * g.W + w] = pl[j];
+  }
+}
+
+__global__ __launch_bounds__(256) void planes_to_ta_kernel(const uint32_t* __restrict__ planes,
+                                                           uint32_t* __restrict__ ta, Geom g) {
+  const int64_t total = g.C * g.L;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t c = idx / g.L, l = idx % g.L;
+    const int64_t w = l >> 5;
+    const int b = (int)(l & 31);
+    uint32_t s = 0u;
+    for (int j = 0; j < g.np; ++j) s |= ((planes[(c * g.np + j) * g.W + w] >> b) & 1u) << j;
+    ta[idx] = s - g.off;
+  }
+}
+
+// Initial state: every TA at number_of_ta_states/2 (src/cutm/base.py:208-209) and the
+// weights of init_weights (kernel.cu:46-73) with its random bit taken from the INIT site.
+__global__ __launch_bounds__(256) void init_state_kernel(uint32_t* __restrict__ planes,
+                                                         float* __restrict__ w, Geom g, uint64_t seed) {
+  const int64_t nplane = g.C * g.W;
+  const int64_t total = nplane > g.C * g.K ? nplane : g.C * g.K;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    if (idx < nplane) {
+      const int64_t c = idx / g.W, wd = idx % g.W;
+      const uint32_t valid = wd == g.W - 1 ? g.last_filter : 0xFFFFFFFFu;
+      const uint32_t s_on = (uint32_t)g.half_state + g.off, s_off = g.off;
+      for (int j = 0; j < g.np; ++j) {
+        const uint32_t v = (((s_on >> j) & 1u) ? valid : 0u) | (((s_off >> j) & 1u) ? ~valid : 0u);
+        planes[(c * g.np + j) * g.W + wd] = v;
+      }
+    }
+    if (idx < g.C * g.K) {
+      const int64_t c = idx / g.K, k = idx % g.K;
+      float v;
+      if (g.coalesced) {
+        v = 1.0f;
+        if (g.init_neg_weights) {
+          const U4 z = site_words(seed, 0, (uint32_t)c, TAG_INIT, (uint32_t)k);
+          v = 1.0f - 2.0f * (float)(z.x & 1u);
+        }
+      } else if (k == c / g.per_bank) {
+        v = 1.0f;
+        if (g.init_neg_weights && (c % g.per_bank) >= (g.per_bank / 2)) v = -1.0f;
+      } else {
+        v = 0.0f;
+      }
+      w[idx] = v;
+    }
+  }
+}
+
+// Number of included literals per clause (pack_clauses' total_count, kernel.cu:166-202).
+__global__ __launch_bounds__(256) void ninc_kernel(const uint32_t* __restrict__ planes,
+                                                   int32_t* __restrict__ ninc, Geom g) {
+  const int lane = lane_id();
+  const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / kWave;
+  const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
+  for (int64_t c = wave; c < g.C; c += nwaves) {
+    const uint32_t* m = planes + (c * g.np + g.np - 1) * g.W;
+    int cnt = 0;
+    for (int64_t w = lane; w < g.W; w += kWave) cnt += __popc(m[w]);
+    cnt = wave_sum_i32(cnt);
+    if (lane == 0) ninc[c] = cnt;
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_u64_kernel(unsigned long long* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0ull;
+}
+
+// ======================================================================== inference
+// Does a non-empty clause (include mask m) match sample xe on at least one patch?
+// clause_match (kernel.cu:207-216) with the early exit of calc_class_sums_infer_batch
+// (kernel.cu:330-336).  Wave-uniform result.
+template <bool VANILLA>
+__device__ __forceinline__ bool clause_fires_any(const uint32_t* __restrict__ m,
+                                                 const uint32_t* __restrict__ xe, const Geom& g) {
+  const int lane = lane_id();
+  if (VANILLA) {
+    uint32_t bad = 0u;
+    for (int64_t w = lane; w < g.W; w += kWave) bad |= m[w] & ~xe[w];
+    return !__any(bad != 0u);
+  } else {
+    for (int64_t base = 0; base < g.P; base += kWave) {
+      const int64_t p = base + lane;
+      bool ok = p < g.P;
+      if (ok) {
+        const uint32_t* xp = xe + p * g.W;
+        for (int64_t w = 0; w < g.W; ++w)
+          if (m[w] & ~xp[w]) {
+            ok = false;
+            break;
+          }
+      }
+      if (__any(ok)) return true;
+    }
+    return false;
+  }
+}
+
+constexpr int kScoreChunk = 256;
+
+// One block per (sample, chunk of clauses); waves take clauses; lane k accumulates the
+// weight of class k over the firing clauses; integer atomics make the sum exact and
+// order-independent.
+template <bool VANILLA>
+__global__ __launch_bounds__(256) void score_kernel(const uint32_t* __restrict__ planes,
+                                                    const int32_t* __restrict__ ninc,
+                                                    const float* __restrict__ w,
+                                                    const uint32_t* __restrict__ X, int64_t N, Geom g,
+                                                    long long* __restrict__ acc) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  const int64_t nch = (g.C + kScoreChunk - 1) / kScoreChunk;
+  for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
+    const int64_t e = blk / nch, ch = blk % nch;
+    const int64_t c0 = ch * kScoreChunk;
+    const int64_t c1 = c0 + kScoreChunk < g.C ? c0 + kScoreChunk : g.C;
+    const uint32_t* xe = X + e * g.P * g.W;
+    long long sum = 0;
+    for (int64_t c = c0 + wave; c < c1; c += nw) {
+      if (ninc[c] == 0) continue;  // empty clauses do not vote (kernel.cu:328)
+      if (clause_fires_any<VANILLA>(planes + (c * g.np + g.np - 1) * g.W, xe, g))
+        if (lane < g.K) sum += (long long)w[c * g.K + lane];
+    }
+    if (lane < g.K && sum != 0)
+      atomicAdd((unsigned long long*)&acc[e * g.K + lane], (unsigned long long)sum);
+  }
+}
+
+__global__ __launch_bounds__(256) void score_finish_kernel(const long long* __restrict__ acc,
+                                                           const float* __restrict__ bias, int64_t N,
+                                                           Geom g, float* __restrict__ out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < N * g.K;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = (float)(acc[i] + (long long)bias[i % g.K]);
+}
+
+// transform (kernel.cu:346-368) and transform_patchwise (kernel.cu:370-394).
+template <bool VANILLA, bool PATCHWISE>
+__global__ __launch_bounds__(256) void transform_kernel(const uint32_t* __restrict__ planes,
+                                                        const int32_t* __restrict__ ninc,
+                                                        const uint32_t* __restrict__ X, int64_t N, Geom g,
+                                                        uint32_t* __restrict__ out) {
+  const int lane = lane_id();
+  const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / kWave;
+  const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
+  for (int64_t ec = wave; ec < N * g.C; ec += nwaves) {
+    const int64_t e = ec / g.C, c = ec % g.C;
+    const uint32_t* m = planes + (c * g.np + g.np - 1) * g.W;
+    const uint32_t* xe = X + e * g.P * g.W;
+    const bool empty = ninc[c] == 0;
+    if (!PATCHWISE) {
+      const bool v = empty ? true : clause_fires_any<VANILLA>(m, xe, g);
+      if (lane == 0) out[ec] = v ? 1u : 0u;
+    } else {
+      for (int64_t base = 0; base < g.P; base += kWave) {
+        const int64_t p = base + lane;
+        if (p < g.P) {
+          uint32_t v = 1u;
+          if (!empty) {
+            const uint32_t* xp = xe + p * g.W;
+            for (int64_t w = 0; w < g.W; ++w)
+              if (m[w] & ~xp[w]) {
+                v = 0u;
+                break;
+              }
+          }
+          out[ec * g.P + p] = v;
+        }
+      }
+    }
+  }
+}
+
+// ========================================================================= training
+// Persistent, cooperative kernel: one launch trains N consecutive samples.
+// Workgroup b owns clauses [C*b/G, C*(b+1)/G) for the whole launch.  Per sample:
+//   A. each wave takes own clauses: include mask (top plane) vs the sample, all patches
+//      (fast_eval, kernel.cu:255-282), reservoir choice of the firing patch
+//      (select_active, kernel.cu:285-316), patch weight, partial class sums in LDS;
+//   B. the workgroup adds (1<<44 | partial) into its copy of the sample's class-sum
+//      slots (agent-scope atomics; copies keep contention to ~16 workgroups per word),
+//      then waits until every copy holds its full workgroup count;
+//   C. clip / target / update probability per class (kernel.cu:397,508-529,543-551);
+//   D. feedback on own clauses (clause_update, kernel.cu:531-613): per class in order,
+//      Q-skip and update draws, Type Ia / Ib / II, weight update, and the literal updates
+//      applied bit-sliced to the clause's planes, 32 literals per lane.
+// The only cross-workgroup traffic is the K class sums of each sample.
+
+constexpr int kSpinLimit = 1 << 22;
+
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int t = __shfl_up(v, off);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
+// Literal-decrement mask of one (clause, class) update for the 32 literals of word w:
+// bit b set iff need bit b is set and u(literal 32w+b) <= S_INV.
+template <bool INJECT>
+__device__ __forceinline__ uint32_t literal_draw_mask(const TrainArgs& a, const float* inj, uint32_t need,
+                                                      uint64_t t, int64_t c, int64_t k, int64_t w) {
+  const Geom& g = a.g;
+  if (INJECT) {
+    uint32_t res = 0u;
+    if (need) {
+      const float* u = inj + g.C * g.P + 2 * g.C * g.K + (c * g.K + k) * g.L + w * 32;
+      for (int b = 0; b < 32; ++b)
+        if (((need >> b) & 1u) && (double)u[b] <= g.s_inv) res |= 1u << b;
+    }
+    return res;
+  } else {
+    // u <= S_INV  <=>  q < s_thr for the 24-bit integer q of the literal; decided from the
+    // most significant plane down, 4 planes per Philox call, until no lane of the wave
+    // has an undecided literal.
+    if (g.s_thr >= (1u << 24)) return need;
+    if (g.s_thr == 0u) return 0u;
+    uint32_t lt = 0u, eq = need;
+    for (int grp = 0; grp < 6; ++grp) {
+      if (!__any(eq != 0u)) break;
+      const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_LIT, (uint32_t)((k * g.W + w) * 6 + grp));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 23 - 4 * grp - i;
+        const uint32_t pl = word_of(z, i);
+        if ((g.s_thr >> j) & 1u) {
+          lt |= eq & ~pl;
+          eq &= pl;
+        } else {
+          eq &= ~pl;
+        }
+      }
+    }
+    return lt;
+  }
+}
+
+// Phase A for one clause (wave-uniform): returns the selected patch or -1 and the
+// clause's include count.
+template <bool VANILLA, bool INJECT>
+__device__ int eval_select(const TrainArgs& a, const float* inj, int64_t c, int64_t i, uint64_t t,
+                           int* ninc_out) {
+  const Geom& g = a.g;
+  const int lane = lane_id();
+  const uint32_t* m = a.planes + (c * g.np + g.np - 1) * g.W;
+  const uint32_t* xe = a.X + i * g.P * g.W;
+  const bool dropped = a.drop[c] == 1u;
+  if (VANILLA) {
+    uint32_t bad = 0u;
+    int cnt = 0;
+    for (int64_t w = lane; w < g.W; w += kWave) {
+      const uint32_t mw = m[w];
+      cnt += __popc(mw);
+      bad |= mw & ~xe[w];
+    }
+    const int ninc = wave_sum_i32(cnt);
+    *ninc_out = ninc;
+    const bool any_bad = __any(bad != 0u);
+    if (dropped) return -1;
+    if (ninc != 0 && any_bad) return -1;
+    // One firing patch: its draw must be below 1.0f / 1.
+    const float u = INJECT ? inj[c * g.P] : uniform_from_word(site_words(a.seed, t, (uint32_t)c, TAG_SEL, 0u).x);
+    return u < a.inv_rank[1] ? 0 : -1;
+  } else {
+    int cnt = 0;
+    for (int64_t w = lane; w < g.W; w += kWave) cnt += __popc(m[w]);
+    const int ninc = wave_sum_i32(cnt);
+    *ninc_out = ninc;
+    if (dropped) return -1;
+    // Firing bitmap: lane q keeps bits of patches [64q, 64q+64).
+    unsigned long long myfire = 0ull;
+    int R = 0;
+    const int nch = (int)((g.P + kWave - 1) / kWave);
+    for (int ch = 0; ch < nch; ++ch) {
+      const int64_t p = (int64_t)ch * kWave + lane;
+      bool ok = p < g.P;
+      if (ok && ninc != 0) {
+        const uint32_t* xp = xe + p * g.W;
+        for (int64_t w = 0; w < g.W; ++w)
+          if (m[w] & ~xp[w]) {
+            ok = false;
+            break;
+          }
+      }
+      const unsigned long long b = __ballot(ok);
+      if (lane == ch) myfire = b;
+      R += __popcll(b);
+    }
+    if (R == 0) return -1;
+    // Reservoir: the selected firing patch is the one of highest rank r whose draw is
+    // below 1.0f / r; scan ranks from R downward, 256 ranks (64 Philox calls) at a time.
+    int best = 0;
+    for (int g0 = (R - 1) >> 2; g0 >= 0; g0 -= kWave) {
+      const int gl = g0 - lane;
+      int lb = 0;
+      if (gl >= 0) {
+        if (INJECT) {
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * gl + 1 + j;
+            if (r <= R && inj[c * g.P + (r - 1)] < a.inv_rank[r]) lb = r;
+          }
+        } else {
+          const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * gl + 1 + j;
+            if (r <= R && uniform_from_word(word_of(z, j)) < a.inv_rank[r]) lb = r;
+          }
+        }
+      }
+      best = wave_max_i32(lb);
+      if (best > 0) break;
+    }
+    if (best == 0) return -1;
+    // Patch of the best-th set bit of the firing bitmap.
+    const int pc = lane < nch ? __popcll(myfire) : 0;
+    const int incl = wave_inclusive_scan(pc);
+    const int excl = incl - pc;
+    const bool here = lane < nch && best > excl && best <= incl;
+    const unsigned long long hb = __ballot(here);
+    const int src = __ffsll((long long)hb) - 1;
+    int pos = 0;
+    if (lane == src) {
+      unsigned long long v = myfire;
+      for (int q = 1; q < best - excl; ++q) v &= v - 1ull;
+      pos = src * kWave + __ffsll((long long)v) - 1;
+    }
+    return __shfl(pos, src);
+  }
+}
+
+// Phase D for one non-dropped clause.  Returns true when any Type Ia/Ib/II branch ran.
+template <bool INJECT>
+__device__ bool feedback(const TrainArgs& a, const float* inj, int64_t c, int64_t i, uint64_t t, int sel,
+                         int ninc, const int* s_tgt, const double* s_prob) {
+  const Geom& g = a.g;
+  const int lane = lane_id();
+  const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+  const int kn = g.coalesced ? (int)g.K : 1;
+  const bool o = sel >= 0;
+  const bool small = o && ninc <= g.maxinc;
+  int type = 0;
+  if (lane < kn) {
+    const int64_t k = kb + lane;
+    const int tgt = s_tgt[k];
+    float uq, uu;
+    if (INJECT) {
+      uq = inj[g.C * g.P + c * g.K + k];
+      uu = inj[g.C * g.P + g.C * g.K + c * g.K + k];
+    } else {
+      const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)k);
+      uq = uniform_from_word(z.x);
+      uu = uniform_from_word(z.y);
+    }
+    const bool skip = tgt == -1 && (double)uq > g.q_prob;
+    if (!skip) {
+      float* wp = a.weights + c * g.K + k;
+      float wv = *wp;
+      const int sign = (wv >= 0.0f) - (wv < 0.0f);
+      const bool upd = (double)uu <= s_prob[k];
+      const int ts = tgt * sign;
+      if (upd) {
+        if (ts > 0 && small) {
+          wv += (float)sign * 1.0f;
+          *wp = wv;
+          type = 1;
+        } else if (ts > 0) {
+          type = 2;
+        } else if (ts < 0 && o) {
+          wv -= (float)sign * 1.0f;
+          if (!g.negative_polarity && wv < 1.0f) wv = 1.0f;
+          *wp = wv;
+          type = 3;
+        }
+      }
+    }
+  }
+  const unsigned long long m1a = __ballot(type == 1);
+  const unsigned long long m1b = __ballot(type == 2);
+  const unsigned long long ops = m1a | m1b | __ballot(type == 3);
+  if (ops == 0ull) return false;
+  const uint32_t* xsel = o ? a.X + (i * g.P + sel) * g.W : nullptr;
+  const int np = g.np;
+  for (int64_t wb = 0; wb < g.W; wb += kWave) {
+    const int64_t w = wb + lane;
+    const bool act = w < g.W;
+    const uint32_t F = act ? (w == g.W - 1 ? g.last_filter : 0xFFFFFFFFu) : 0u;
+    uint32_t* pw = a.planes + c * np * g.W + w;
+    uint32_t pl[kMaxPlanes];
+#pragma unroll
+    for (int j = 0; j < kMaxPlanes; ++j) pl[j] = (j < np && act) ? pw[(int64_t)j * g.W] : 0u;
+    const uint32_t xb = (o && act) ? xsel[w] : 0u;
+    unsigned long long rem = ops;
+    while (rem) {
+      const int b = __ffsll((long long)rem) - 1;
+      rem &= rem - 1ull;
+      const int64_t k = kb + b;
+      if ((m1a >> b) & 1ull) {
+        // Type Ia (kernel.cu:410-443): literal 1 -> +1 below MAX, literal 0 -> -1 w.p. 1/s.
+        const uint32_t inc = xb & planes_lt(pl, np, g.max_state_p) & F;
+        const uint32_t need = ~xb & planes_gt(pl, np, g.off) & F;
+        const uint32_t dec = literal_draw_mask<INJECT>(a, inj, need, t, c, k, w);
+        planes_inc(pl, np, inc);
+        planes_dec(pl, np, dec);
+      } else if ((m1b >> b) & 1ull) {
+        // Type Ib (kernel.cu:453-470): every literal -1 w.p. 1/s.
+        const uint32_t need = planes_gt(pl, np, g.off) & F;
+        const uint32_t dec = literal_draw_mask<INJECT>(a, inj, need, t, c, k, w);
+        planes_dec(pl, np, dec);
+      } else {
+        // Type II (kernel.cu:481-506): literal 0 -> +1, no upper guard.
+        planes_inc(pl, np, ~xb & F);
+      }
+    }
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < kMaxPlanes; ++j)
+        if (j < np) pw[(int64_t)j * g.W] = pl[j];
+    }
+  }
+  return true;
+}
+
+template <bool VANILLA, bool INJECT>
+__global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainArgs a) {
+  extern __shared__ long long dyn_lds[];
+  __shared__ long long s_part[64];
+  __shared__ int s_tgt[64];
+  __shared__ double s_prob[64];
+  __shared__ int s_next;
+  __shared__ int s_abort;
+  const Geom& g = a.g;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int G = gridDim.x, wg = blockIdx.x;
+  const int64_t c_begin = g.C * wg / G, c_end = g.C * (wg + 1) / G;
+  const int n_own = (int)(c_end - c_begin);
+  const int copy = wg % a.D;
+  const int nslot = a.D * (int)g.K;
+  long long* s_words = dyn_lds;                        // [D*K]
+  int* s_sel = (int*)(dyn_lds + nslot);                // [cpw]
+  int* s_ninc = s_sel + a.cpw;                         // [cpw]
+  unsigned long long my_updates = 0ull;
+  if (threadIdx.x == 0) s_abort = 0;
+
+  for (int i = 0; i < a.N; ++i) {
+    const uint64_t t = a.step0 + (uint64_t)i;
+    const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
+    if (threadIdx.x < g.K) s_part[threadIdx.x] = 0;
+    if (threadIdx.x == 0) s_next = 0;
+    __syncthreads();
+
+    // ---- A: evaluation, reservoir selection, partial class sums
+    for (;;) {
+      int idx = 0;
+      if (lane == 0) idx = atomicAdd(&s_next, 1);
+      idx = __shfl(idx, 0);
+      if (idx >= n_own) break;
+      const int64_t c = c_begin + idx;
+      int ninc;
+      const int sel = eval_select<VANILLA, INJECT>(a, inj, c, i, t, &ninc);
+      if (lane == 0) {
+        s_sel[idx] = sel;
+        s_ninc[idx] = ninc;
+      }
+      if (sel >= 0) {
+        if (lane == 0) a.patch_w[c * g.P + sel] += 1;
+        if (g.coalesced) {
+          if (lane < g.K)
+            atomicAdd((unsigned long long*)&s_part[lane], (unsigned long long)(long long)a.weights[c * g.K + lane]);
+        } else if (lane == 0) {
+          const int64_t k = c / g.per_bank;
+          atomicAdd((unsigned long long*)&s_part[k], (unsigned long long)(long long)a.weights[c * g.K + k]);
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- B: publish this workgroup's partial class sums, wait for all workgroups
+    unsigned long long* row = a.slots + (int64_t)i * nslot;
+    if (threadIdx.x < g.K)
+      __hip_atomic_fetch_add(&row[copy * g.K + threadIdx.x], (1ull << 44) + (unsigned long long)s_part[threadIdx.x],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wave == 0) {
+      int spins = 0;
+      for (;;) {
+        bool ok = true;
+        for (int q = lane; q < nslot; q += kWave) {
+          const unsigned long long v = __hip_atomic_load(&row[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const int d = q / (int)g.K;
+          const unsigned long long expect = (unsigned long long)((G - d + a.D - 1) / a.D);
+          if (((v + (1ull << 43)) >> 44) != expect)
+            ok = false;
+          else
+            s_words[q] = (long long)(v - (expect << 44));
+        }
+        if (__all(ok)) break;
+        if (++spins > kSpinLimit) {
+          if (lane == 0) {
+            s_abort = 1;
+            atomicOr(a.err, 1);
+          }
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    __syncthreads();
+    if (s_abort) break;
+
+    // ---- C: per-class clip, target and update probability
+    if (threadIdx.x < g.K) {
+      const int k = threadIdx.x;
+      long long S = (long long)a.bias[k];
+      for (int d = 0; d < a.D; ++d) S += s_words[d * g.K + k];
+      const float cs = (float)S;
+      const float v = ((double)cs > g.thresh) ? (float)g.thresh : (((double)cs < -g.thresh) ? (float)(-g.thresh) : cs);
+      const int y = a.Y[(int64_t)i * g.K + k];
+      s_tgt[k] = 1 - 2 * (v > (float)y);
+      s_prob[k] = ((double)y - (double)v) / (2.0 * (double)y);
+    }
+    if (threadIdx.x == 0) s_next = 0;
+    __syncthreads();
+
+    // ---- D: feedback
+    for (;;) {
+      int idx = 0;
+      if (lane == 0) idx = atomicAdd(&s_next, 1);
+      idx = __shfl(idx, 0);
+      if (idx >= n_own) break;
+      const int64_t c = c_begin + idx;
+      if (a.drop[c] == 1u) continue;
+      const bool touched = feedback<INJECT>(a, inj, c, i, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob);
+      if (touched && lane == 0) ++my_updates;
+    }
+    __syncthreads();
+  }
+  if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
+}
+
+// ========================================================================= launchers
+static int grid_for(int64_t items, int block) {
+  int64_t g = (items + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > 65536) g = 65536;
+  return (int)g;
+}
+
+hipError_t launch_encode(const uint32_t* X, int64_t N, uint32_t* out, const Geom& g, hipStream_t s) {
+  encode_kernel<<<grid_for(N * g.P * g.W, 256), 256, 0, s>>>(X, N, out, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_ta_to_planes(const uint32_t* ta, uint32_t* planes, const Geom& g, hipStream_t s) {
+  ta_to_planes_kernel<<<grid_for(g.C * g.W, 256), 256, 0, s>>>(ta, planes, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_planes_to_ta(const uint32_t* planes, uint32_t* ta, const Geom& g, hipStream_t s) {
+  planes_to_ta_kernel<<<grid_for(g.C * g.L, 256), 256, 0, s>>>(planes, ta, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_init_state(uint32_t* planes, float* w, const Geom& g, uint64_t seed, hipStream_t s) {
+  const int64_t n = g.C * g.W > g.C * g.K ? g.C * g.W : g.C * g.K;
+  init_state_kernel<<<grid_for(n, 256), 256, 0, s>>>(planes, w, g, seed);
+  return hipGetLastError();
+}
+
+hipError_t launch_ninc(const uint32_t* planes, int32_t* ninc, const Geom& g, hipStream_t s) {
+  ninc_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, ninc, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s) {
+  fill_u64_kernel<<<grid_for(n, 256), 256, 0, s>>>(p, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_score(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
+                        int64_t N, const Geom& g, long long* acc, hipStream_t s) {
+  const int64_t blocks = N * ((g.C + kScoreChunk - 1) / kScoreChunk);
+  const int grid = blocks < 65536 ? (int)blocks : 65536;
+  if (g.P == 1)
+    score_kernel<true><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc);
+  else
+    score_kernel<false><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc);
+  return hipGetLastError();
+}
+
+hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t N, const Geom& g, float* out,
+                               hipStream_t s) {
+  score_finish_kernel<<<grid_for(N * g.K, 256), 256, 0, s>>>(acc, bias, N, g, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const uint32_t* X, int64_t N,
+                            const Geom& g, int patchwise, uint32_t* out, hipStream_t s) {
+  const int grid = grid_for(N * g.C * kWave, 256);
+  if (g.P == 1) {
+    if (patchwise)
+      transform_kernel<true, true><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
+    else
+      transform_kernel<true, false><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
+  } else {
+    if (patchwise)
+      transform_kernel<false, true><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
+    else
+      transform_kernel<false, false><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
+  }
+  return hipGetLastError();
+}
+
+size_t train_lds_bytes(int cpw, int D, int K) {
+  return (size_t)D * K * sizeof(long long) + (size_t)2 * cpw * sizeof(int);
+}
+
+static const void* train_fn(bool vanilla, bool inject) {
+  if (vanilla) return inject ? (const void*)train_kernel<true, true> : (const void*)train_kernel<true, false>;
+  return inject ? (const void*)train_kernel<false, true> : (const void*)train_kernel<false, false>;
+}
+
+hipError_t train_occupancy(bool vanilla, bool inject, size_t lds_bytes, int* blocks_per_cu) {
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, train_fn(vanilla, inject), kTrainThreads,
+                                                      lds_bytes);
+}
+
+hipError_t launch_train(const TrainArgs& a, int grid, size_t lds_bytes, bool vanilla, bool inject, hipStream_t s) {
+  TrainArgs copy = a;
+  void* args[] = {&copy};
+  return hipLaunchCooperativeKernel(train_fn(vanilla, inject), dim3(grid), dim3(kTrainThreads), args,
+                                    (unsigned)lds_bytes, s);
+}
+
+}  // namespace ytm
