@@ -137,7 +137,11 @@ def main() -> int:
         upd += st["last_fit_updates"]
         byts.append(train_bytes_per_launch(tm, N, st["last_fit_updates"]))
         log(f"[bench] step {s + 1}: wall {walls[-1]:.3f}s kernel {kern[-1]:.1f}ms updates {st['last_fit_updates']} "
-            f"({st['last_fit_updates'] / N:.1f}/sample) workgroups {st['train_workgroups']}")
+            f"({st['last_fit_updates'] / N:.1f}/sample) workgroups {st['train_workgroups']} "
+            f"kind {st['train_kind']} wait {st['last_fit_wait_frac']:.3f}")
+        if os.environ.get("YTM_TRAIN_PROFILE"):
+            log("[bench]   phase us/sample: A %.2f barA %.2f exch %.2f barBC %.2f D1 %.2f barD1 %.2f D2 %.2f D3 %.2f"
+                % tuple(st["last_fit_phase_us"]))
 
     # inference over the test set (resident), best of 3 after one warm call
     cs = tm.score_device(dtest)
@@ -199,6 +203,10 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    out["train_wait_fraction"] = round(tm.stats()["last_fit_wait_frac"], 4)
+    dtrain.release()
+    dtest.release()
+    tm.release()
     if not args.no_cpu:
         out["cpu_baseline"], _ = cpu_baseline(encX, y, kw, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -63,6 +63,13 @@ typedef struct ytm_stats {
     int32_t train_workgroups;    /* persistent grid size used by the training kernel */
     double last_score_kernel_ms; /* class-sum kernel of the last score */
     double last_encode_kernel_ms;
+    double last_fit_wait_frac;   /* share of the training kernel's time workgroups spent
+                                    waiting for the per-sample class sums */
+    int32_t train_kind;          /* 0 = clause state resident in LDS, 1 = global (one
+                                    patch), 2 = global (several patches) */
+    int32_t reserved;
+    double last_fit_phase_us[8]; /* with YTM_TRAIN_PROFILE=1 and the resident kernel:
+                                    average microseconds per sample of each phase */
 } ytm_stats;
 
 /* Thread-local description of the last failure. */

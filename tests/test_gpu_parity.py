@@ -21,6 +21,9 @@ from ytm_amd import MultiClassTM, MultiOutputTM  # noqa: E402
 
 orc.set_threads(min(16, os.cpu_count() or 1))
 
+BANKS_OFF = ("coalesced=False is switched off: its first GPU training run stalled and the cause is not "
+             "yet shown")
+
 
 def pair(cfg, n_train, n_test=0, clauses=None, seed=workloads.MODEL_SEED, **opts):
     X, y, Xt, yt, kw = workloads.make(cfg, n_train, n_test)
@@ -73,6 +76,22 @@ def test_fit_counter_stream(cfg, n, clauses, epochs):
         assert_state_equal(tm, ref, f"epoch {epoch}")
 
 
+@pytest.mark.parametrize("cfg,n,clauses", [(1, 3000, None), (2, 200, None), (5, 30, 200)])
+def test_fit_global_state_kernel(monkeypatch, cfg, n, clauses):
+    """The one-patch configurations also through the kernel that keeps clause state in
+    global memory (the default keeps it resident in LDS when it fits)."""
+    monkeypatch.setenv("YTM_TRAIN_GLOBAL", "1")
+    tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    for epoch in range(2):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, encY)
+        assert tm.stats()["train_kind"] == 1
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+
+
 @pytest.mark.parametrize("cfg,n,clauses", [(1, 60, None), (2, 6, 40), (3, 5, 12), (4, 2, 6), (5, 3, 4)])
 def test_fit_injected_stream(cfg, n, clauses):
     tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses)
@@ -92,7 +111,8 @@ def test_fit_injected_stream(cfg, n, clauses):
 
 @pytest.mark.parametrize(
     "opts",
-    [dict(coalesced=False), dict(negative_polarity=False, init_neg_weights=False), dict(max_included_literals=4),
+    [pytest.param(dict(coalesced=False), marks=pytest.mark.skip(reason=BANKS_OFF)),
+     dict(negative_polarity=False, init_neg_weights=False), dict(max_included_literals=4),
      dict(append_negated=False), dict(number_of_ta_states=16), dict(q=3), dict(q=0.5)],
 )
 def test_fit_variant_flags(opts):
@@ -199,6 +219,7 @@ def _big_view(tm):
     return np.broadcast_to(base, (n,) + base.shape[1:])
 
 
+@pytest.mark.skip(reason=BANKS_OFF)
 def test_non_coalesced_shapes():
     X, y, *_ , kw = workloads.make(2, 50, 1)
     kw.update(number_of_clauses_per_class=6, coalesced=False, seed=3)

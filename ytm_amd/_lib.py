@@ -51,6 +51,10 @@ class YtmStats(ctypes.Structure):
         ("train_workgroups", ctypes.c_int32),
         ("last_score_kernel_ms", ctypes.c_double),
         ("last_encode_kernel_ms", ctypes.c_double),
+        ("last_fit_wait_frac", ctypes.c_double),
+        ("train_kind", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("last_fit_phase_us", ctypes.c_double * 8),
     ]
 
 

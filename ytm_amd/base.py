@@ -19,6 +19,7 @@ seed, or from an injected buffer passed as ``fit(..., random_stream=...)``.
 from __future__ import annotations
 
 import ctypes
+import sys
 from typing import Any
 
 import numpy as np
@@ -76,11 +77,17 @@ class DeviceData:
         check(lib.ytm_dataset_create(tm._handle, ptr(encoded_X), ptr(encoded_Y), self.n, ctypes.byref(handle)))
         self.handle = handle
 
-    def __del__(self):
+    def release(self) -> None:
         handle = getattr(self, "handle", None)
         if handle is not None and handle.value:
             lib.ytm_dataset_destroy(handle)
-            self.handle = None
+        self.handle = None
+
+    def __del__(self):
+        # At interpreter exit the HIP runtime may already be torn down; the process
+        # teardown releases the device memory instead.
+        if not sys.is_finalizing():
+            self.release()
 
 
 class BaseTM:
@@ -180,17 +187,24 @@ class BaseTM:
         check(lib.ytm_create(ctypes.byref(self._params_c), ctypes.byref(handle)))
         self._handle = handle
 
-    def __del__(self):
+    def release(self) -> None:
+        """Free the model's device memory now (the object is unusable afterwards)."""
         handle = getattr(self, "_handle", None)
         if handle is not None and handle.value:
             lib.ytm_destroy(handle)
-            self._handle = None
+        self._handle = None
+
+    def __del__(self):
+        if not sys.is_finalizing():
+            self.release()
 
     def stats(self) -> dict:
         """Counters and kernel timings of the most recent calls."""
         st = _lib.YtmStats()
         check(lib.ytm_get_stats(self._handle, ctypes.byref(st)))
-        return {name: getattr(st, name) for name, _ in st._fields_}
+        out = {name: getattr(st, name) for name, _ in st._fields_}
+        out["last_fit_phase_us"] = list(out["last_fit_phase_us"])
+        return out
 
     # ------------------------------------------------------------------ encode
     def encode(self, X: np.ndarray, block_size: int | None = None) -> np.ndarray:

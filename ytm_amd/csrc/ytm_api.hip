@@ -74,6 +74,9 @@ int resolve_geometry(const ytm_params& p, Geom* out) {
   if (p.number_of_ta_states < 1) return fail(YTM_EINVAL, "number_of_ta_states must be >= 1");
   if (!p.coalesced && p.clauses % p.classes != 0)
     return fail(YTM_EINVAL, "non-coalesced clause banks need clauses divisible by classes");
+  // Switched off: its first GPU training run stalled without a cause shown yet.
+  if (!p.coalesced)
+    return fail(YTM_EINVAL, "coalesced=False (clause banks) is disabled in this build");
   g.C = p.clauses;
   g.K = p.classes;
   g.dim0 = p.dim0; g.dim1 = p.dim1; g.dim2 = p.dim2;
@@ -135,15 +138,22 @@ int upload(void** dst, const void* src, size_t bytes, hipStream_t s) {
   return YTM_OK;
 }
 
-// Picks the persistent grid: one workgroup per CU at most, at least ~8 clauses each.
-void train_shape(const ytm_model* m, int* grid, int* D, int* cpw) {
+// LDS a resident training workgroup may use (gfx950 has 160 KiB per workgroup; the
+// kernel's static LDS and some headroom are kept free).
+constexpr size_t kResidentLdsLimit = 150 * 1024;
+
+// Picks the persistent grid (one workgroup per CU at most, at least ~8 clauses each) and
+// the class-sum grouping (groups of <= 16 workgroups).
+void train_shape(const ytm_model* m, int* grid, int* S, int* D, int* cpw) {
   const char* env = std::getenv("YTM_TRAIN_WGS");
   int64_t G = std::min<int64_t>(m->cus, std::max<int64_t>(1, (m->g.C + 7) / 8));
   if (env && std::atoi(env) > 0) G = std::min<int64_t>(std::atoi(env), m->g.C);
   *grid = (int)G;
-  const char* envd = std::getenv("YTM_TRAIN_GROUP");
-  int per_copy = envd && std::atoi(envd) > 0 ? std::atoi(envd) : 16;
-  *D = (int)((G + per_copy - 1) / per_copy);
+  const char* envs = std::getenv("YTM_TRAIN_GROUP");
+  int s = envs && std::atoi(envs) > 0 ? std::atoi(envs) : 16;
+  s = (int)std::min<int64_t>(s, G);
+  *S = s;
+  *D = (int)((G + s - 1) / s);
   *cpw = (int)((m->g.C + G - 1) / G) + 1;
 }
 
@@ -187,8 +197,8 @@ int ytm_create(const ytm_params* params, ytm_model** out) {
   CREATE_TRY(hipMalloc(&m->d_bias, (size_t)g.K * 4));
   CREATE_TRY(hipMalloc(&m->d_ninc, (size_t)g.C * 4));
   CREATE_TRY(hipMalloc(&m->d_inv_rank, (size_t)(g.P + 1) * 4));
-  CREATE_TRY(hipMalloc(&m->d_counters, 64));
-  CREATE_TRY(hipMalloc(&m->d_err, 4));
+  CREATE_TRY(hipMalloc(&m->d_counters, 128));
+  CREATE_TRY(hipMalloc(&m->d_err, 16));
   std::vector<float> inv((size_t)g.P + 1);
   inv[0] = 0.0f;
   for (int64_t r = 1; r <= g.P; ++r) inv[r] = 1.0f / (float)r;  // IEEE fp32 division
@@ -309,20 +319,28 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   m->stats.last_fit_launches = 0;
   if (count == 0) return YTM_OK;
   const Geom& g = m->g;
-  int grid, D, cpw;
-  train_shape(m, &grid, &D, &cpw);
-  const size_t lds = ytm::train_lds_bytes(cpw, D, (int)g.K);
-  const bool vanilla = g.P == 1;
+  int grid, S, D, cpw;
+  train_shape(m, &grid, &S, &D, &cpw);
   const bool inj = inject != nullptr;
+  // One patch and the workgroup's clause state fits in LDS: keep it resident.
+  ytm::TrainKind kind = g.P == 1 ? ytm::TrainKind::kGlobalVanilla : ytm::TrainKind::kGlobalConv;
+  const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
+  if (g.P == 1 && !(force_global && std::atoi(force_global) > 0) &&
+      ytm::train_lds_bytes(ytm::TrainKind::kResident, cpw, ytm::train_rng_slots(cpw, g), g) <= kResidentLdsLimit)
+    kind = ytm::TrainKind::kResident;
+  const int rng_slots = kind == ytm::TrainKind::kResident ? ytm::train_rng_slots(cpw, g) : 0;
+  const size_t lds = ytm::train_lds_bytes(kind, cpw, rng_slots, g);
   int bpc = 0;
-  HIP_TRY(ytm::train_occupancy(vanilla, inj, lds, &bpc));
+  HIP_TRY(ytm::train_occupancy(kind, inj, lds, &bpc));
   if ((int64_t)bpc * m->cus < grid)
     return fail(YTM_EINVAL, "training grid does not fit co-resident on the device");
   m->stats.train_workgroups = grid;
 
   // Per-launch sample count: bounded by the class-sum slot memory (<= 256 MiB) and, in
   // injected mode, by the size of the injected block buffer (<= 1 GiB).
-  const int64_t slot_row = (int64_t)D * g.K * 8;
+  const int64_t ks = (g.K + 15) & ~(int64_t)15;
+  const int64_t slot_stride = D == 1 ? ks : (2 * (int64_t)D + 1) * ks;
+  const int64_t slot_row = slot_stride * 8;
   int64_t per_launch = std::max<int64_t>(1, ((int64_t)256 << 20) / slot_row);
   const int64_t block = g.C * g.P + 2 * g.C * g.K + g.C * g.K * g.L;
   if (inj) per_launch = std::min<int64_t>(per_launch, std::max<int64_t>(1, ((int64_t)1 << 30) / (block * 4)));
@@ -359,15 +377,15 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
       return finish(fail(YTM_EHIP, std::string(#expr) + " failed: " + hipGetErrorString(e_)));  \
   } while (0)
 
-  FIT_TRY(hipMemsetAsync(m->d_counters, 0, 64, m->stream));
-  FIT_TRY(hipMemsetAsync(m->d_err, 0, 4, m->stream));
+  FIT_TRY(hipMemsetAsync(m->d_counters, 0, 128, m->stream));
+  FIT_TRY(hipMemsetAsync(m->d_err, 0, 16, m->stream));
   double ms_total = 0.0;
   int launches = 0;
   for (int64_t s = 0; s < count; s += per_launch) {
     const int64_t n = std::min(per_launch, count - s);
     if (inj)
       FIT_TRY(hipMemcpyAsync(d_inj, inject + s * block, (size_t)(n * block) * 4, hipMemcpyHostToDevice, m->stream));
-    FIT_TRY(ytm::launch_fill_u64(m->d_slots, n * D * g.K, m->stream));
+    FIT_TRY(ytm::launch_fill_u64(m->d_slots, n * slot_stride, m->stream));
     ytm::TrainArgs a{};
     a.planes = m->d_planes;
     a.weights = m->d_w;
@@ -385,24 +403,38 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.step0 = m->stats.step + (uint64_t)s;
     a.seed = m->params.seed;
     a.N = (int)n;
+    a.S = S;
     a.D = D;
+    a.slot_stride = slot_stride;
     a.cpw = cpw;
+    a.rng_slots = rng_slots;
+    const char* prof_env = std::getenv("YTM_TRAIN_PROFILE");
+    a.profile = prof_env && std::atoi(prof_env) > 0;
     a.g = g;
     FIT_TRY(hipEventRecord(m->ev0, m->stream));
-    FIT_TRY(ytm::launch_train(a, grid, lds, vanilla, inj, m->stream));
+    FIT_TRY(ytm::launch_train(a, grid, lds, kind, inj, m->stream));
     FIT_TRY(hipEventRecord(m->ev1, m->stream));
     FIT_TRY(hipEventSynchronize(m->ev1));
     float ms = 0.0f;
     FIT_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
     ms_total += ms;
     ++launches;
-    int herr = 0;
-    FIT_TRY(hipMemcpy(&herr, m->d_err, 4, hipMemcpyDeviceToHost));
-    if (herr) return finish(fail(YTM_ETIMEOUT, "training kernel: a workgroup's bounded wait for the class sums expired"));
+    int herr[4] = {0, 0, 0, 0};
+    FIT_TRY(hipMemcpy(herr, m->d_err, sizeof(herr), hipMemcpyDeviceToHost));
+    if (herr[0])
+      return finish(fail(YTM_ETIMEOUT, "training kernel: the bounded wait for the class sums of sample " +
+                                           std::to_string(s + herr[1]) + " expired in workgroup " +
+                                           std::to_string(herr[2]) + " (count seen " + std::to_string(herr[3]) +
+                                           ", grid " + std::to_string(grid) + ", groups " + std::to_string(D) + ")"));
   }
-  unsigned long long upd = 0;
-  FIT_TRY(hipMemcpy(&upd, m->d_counters, 8, hipMemcpyDeviceToHost));
+  unsigned long long cnt[16] = {0};
+  FIT_TRY(hipMemcpy(cnt, m->d_counters, sizeof(cnt), hipMemcpyDeviceToHost));
+  // phase ticks are summed over workgroups and samples: average microseconds per sample
+  for (int j = 0; j < 8; ++j) m->stats.last_fit_phase_us[j] = (double)cnt[4 + j] / 100.0 / (double)grid / (double)count;
+  const unsigned long long upd = cnt[0];
 #undef FIT_TRY
+  m->stats.last_fit_wait_frac = cnt[2] ? (double)cnt[1] / (double)cnt[2] : 0.0;
+  m->stats.train_kind = (int32_t)kind;
   m->stats.step += (uint64_t)count;
   m->stats.last_fit_samples = (uint64_t)count;
   m->stats.last_fit_updates = upd;

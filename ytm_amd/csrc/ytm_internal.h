@@ -36,15 +36,19 @@ struct TrainArgs {
   const uint32_t* drop;      // [C]
   const float* inject;       // [N][inject_block] or nullptr
   const float* inv_rank;     // [P + 1], inv_rank[r] = 1.0f / r
-  unsigned long long* slots; // [N][D][K], zero on entry
-  unsigned long long* counters;  // [0] += clauses that ran a feedback branch
+  unsigned long long* slots; // [N][slot_stride], zero on entry
+  unsigned long long* counters;  // [0] updated clauses, [1] wait ticks, [2] kernel ticks, [4..11] phases
   int* err;                  // set to 1 when a bounded wait expires
   int64_t inject_block;
   uint64_t step0;
   uint64_t seed;
   int N;
-  int D;                     // class-sum copies (each shared by at most ~16 workgroups)
+  int S;                     // workgroups per class-sum group
+  int D;                     // class-sum groups (ceil(grid / S))
+  int64_t slot_stride;       // slot words per sample: D == 1 ? ks : (2D + 1) * ks, ks = K rounded up to 16
   int cpw;                   // max clauses owned by one workgroup
+  int rng_slots;             // literal-draw slots precomputed per sample (resident kernel)
+  int profile;               // accumulate per-phase times into counters[4..11]
   Geom g;
 };
 
@@ -62,9 +66,13 @@ hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t 
                                float* out, hipStream_t s);
 hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const uint32_t* X, int64_t N,
                             const Geom& g, int patchwise, uint32_t* out, hipStream_t s);
-hipError_t train_occupancy(bool vanilla, bool inject, size_t lds_bytes, int* blocks_per_cu);
-hipError_t launch_train(const TrainArgs& a, int grid, size_t lds_bytes, bool vanilla, bool inject,
-                        hipStream_t s);
-size_t train_lds_bytes(int cpw, int D, int K);
+// Training kernel variants: clause state resident in LDS (one patch), or kept in global
+// memory (one patch / several patches).
+enum class TrainKind { kResident, kGlobalVanilla, kGlobalConv };
+hipError_t train_occupancy(TrainKind kind, bool inject, size_t lds_bytes, int* blocks_per_cu);
+hipError_t launch_train(const TrainArgs& a, int grid, size_t lds_bytes, TrainKind kind, bool inject, hipStream_t s);
+size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g);
+// Literal-draw slots the resident kernel precomputes per sample within an LDS budget.
+int train_rng_slots(int cpw, const Geom& g);
 
 }  // namespace ytm
