@@ -67,7 +67,9 @@ typedef struct ytm_stats {
                                     waiting for the per-sample class sums */
     int32_t train_kind;          /* 0 = clause state resident in LDS, 1 = global (one
                                     patch), 2 = global (several patches) */
-    int32_t reserved;
+    int32_t train_specialised;   /* 1 when the last fit ran a training kernel compiled at run
+                                    time for this model's geometry (hipRTC), 0 when it ran the
+                                    built-in kernel (YTM_JIT=0, or the compile was unavailable) */
     double last_fit_phase_us[8]; /* with YTM_TRAIN_PROFILE=1 and the resident kernel:
                                     average microseconds per sample of each phase */
 } ytm_stats;
@@ -85,6 +87,14 @@ int ytm_geometry(const ytm_model *m, int64_t out[4]);
 int ytm_get_stats(const ytm_model *m, ytm_stats *out);
 /* Reseed the random stream and reset its step to 0 (what re-running __init__ does). */
 int ytm_set_seed(ytm_model *m, uint64_t seed);
+/* Compile (and cache for this process) the training kernel specialised for the geometry
+ * of *params, without touching a GPU.  train_kind as in ytm_stats (0 resident, 1 global
+ * one patch, 2 global several patches); injected != 0 for the injected-draw variant.
+ * The counterpart of the per-model kernel compile in BaseTM.__init__
+ * (src/cutm/base.py:129-159); ytm_fit compiles on first use anyway, so calling this is
+ * optional (warm-up, or checking that the compiler is available).  YTM_EHIP with the
+ * compiler log in ytm_last_error() on failure. */
+int ytm_compile_train_kernel(const ytm_params *params, int train_kind, int injected);
 
 /* encode: BaseTM.encode (src/cutm/base.py:224-263; kernel.cu:76-152 encode_batch).
  * X: uint32 (N, dim0*dim1*dim2), any value > 0 is a set pixel.  out: uint32 (N, P, W). */

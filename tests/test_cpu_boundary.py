@@ -56,6 +56,30 @@ def test_error_without_gpu_is_raised_not_swallowed():
         pytest.skip("a GPU is visible; covered by the gpu tests")
 
 
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_specialised_training_kernels_compile(cfg):
+    """hipRTC compiles the per-model training kernels (both draw modes) without a GPU."""
+    import workloads
+    from ytm_amd import MultiClassTM
+
+    kw = workloads.make(cfg, 2, 2)[4]
+    for injected in (False, True):
+        kinds = MultiClassTM.compile_kernels(**kw, injected=injected)
+        assert kinds == ([2] if cfg in (3, 4) else [0, 1])
+
+
+def test_compile_entry_point_rejects_bad_kind():
+    from ytm_amd import MultiClassTM, _lib
+
+    tm = MultiClassTM.__new__(MultiClassTM)
+    tm._skip_gpu_init = True
+    tm.__init__(10, 15, 3.9, (12, 1, 1), 2, seed=1)
+    params = tm._params()
+    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 2, 0) == 1  # several patches only
+    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 7, 0) == 1
+    assert b"train_kind" in _lib.lib.ytm_last_error()
+
+
 @pytest.mark.parametrize(
     "s,expected",
     [

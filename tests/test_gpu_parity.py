@@ -25,6 +25,13 @@ BANKS_OFF = ("coalesced=False is switched off: its first GPU training run stalle
              "yet shown")
 
 
+@pytest.fixture(autouse=True)
+def _specialised_kernels_required(monkeypatch):
+    """Training runs the kernels compiled per model (hipRTC); a failed compile is an error
+    here rather than a silent switch to the built-in kernels (tested on their own below)."""
+    monkeypatch.setenv("YTM_JIT", "2")
+
+
 def pair(cfg, n_train, n_test=0, clauses=None, seed=workloads.MODEL_SEED, **opts):
     X, y, Xt, yt, kw = workloads.make(cfg, n_train, n_test)
     if clauses is not None:
@@ -90,6 +97,40 @@ def test_fit_global_state_kernel(monkeypatch, cfg, n, clauses):
         assert tm.stats()["train_kind"] == 1
         assert tm.stats()["last_fit_updates"] == upd
         assert_state_equal(tm, ref, f"epoch {epoch}")
+
+
+@pytest.mark.parametrize("cfg,n,clauses,global_state,inject",
+                         [(1, 2000, None, False, False), (1, 1000, None, True, False), (2, 150, None, False, False),
+                          (2, 100, None, True, False), (3, 40, 100, False, False), (5, 30, 200, False, False),
+                          (1, 40, None, False, True), (3, 4, 12, False, True)])
+def test_fit_builtin_kernels(monkeypatch, cfg, n, clauses, global_state, inject):
+    """The built-in training kernels (geometry read from the kernel arguments) give the
+    same results as the per-model compiled ones: both against the oracle."""
+    monkeypatch.setenv("YTM_JIT", "0")
+    if global_state:
+        monkeypatch.setenv("YTM_TRAIN_GLOBAL", "1")
+    tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    rng = np.random.default_rng(cfg)
+    for epoch in range(2):
+        inj = rng.random(tm.random_stream_size(n)).astype(np.float32) if inject else None
+        tm.fit(encX, y, is_X_encoded=True, random_stream=inj)
+        upd = ref.fit_encoded(encX, encY, inject=inj)
+        st = tm.stats()
+        assert st["train_specialised"] == 0
+        if tm.number_of_patches > 1:
+            assert st["train_kind"] == 2
+        elif global_state:
+            assert st["train_kind"] == 1
+        assert st["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+
+
+def test_specialised_kernel_is_used():
+    tm, ref, X, y, *_ = pair(2, 20)
+    tm.fit(tm.encode(X), y, is_X_encoded=True)
+    assert tm.stats()["train_specialised"] == 1
 
 
 @pytest.mark.parametrize("cfg,n,clauses", [(1, 60, None), (2, 6, 40), (3, 5, 12), (4, 2, 6), (5, 3, 4)])

@@ -53,7 +53,7 @@ class YtmStats(ctypes.Structure):
         ("last_encode_kernel_ms", ctypes.c_double),
         ("last_fit_wait_frac", ctypes.c_double),
         ("train_kind", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("train_specialised", ctypes.c_int32),
         ("last_fit_phase_us", ctypes.c_double * 8),
     ]
 
@@ -68,6 +68,7 @@ SIGNATURES = {
     "ytm_geometry": (ctypes.c_int, [_P, _P]),
     "ytm_get_stats": (ctypes.c_int, [_P, ctypes.POINTER(YtmStats)]),
     "ytm_set_seed": (ctypes.c_int, [_P, ctypes.c_uint64]),
+    "ytm_compile_train_kernel": (ctypes.c_int, [ctypes.POINTER(YtmParams), ctypes.c_int, ctypes.c_int]),
     "ytm_encode": (ctypes.c_int, [_P, _P, _I64, _P]),
     "ytm_dataset_create": (ctypes.c_int, [_P, _P, _P, _I64, ctypes.POINTER(_P)]),
     "ytm_dataset_destroy": (None, [_P]),

@@ -181,7 +181,25 @@ class BaseTM:
         p.seed = key
         return p
 
+    @classmethod
+    def compile_kernels(cls, *args, injected: bool = False, **kwargs) -> list[int]:
+        """Compile and cache, for this process, the training kernels specialised for a model
+        built with these arguments; needs no GPU (the counterpart of the per-model compile
+        in the reference's BaseTM.__init__, src/cutm/base.py:129-159).  Fitting compiles on
+        first use anyway.  Returns the training-kernel kinds compiled."""
+        tm = cls.__new__(cls)
+        tm._skip_gpu_init = True
+        tm.__init__(*args, **kwargs)
+        params = tm._params()
+        kinds = [0, 1] if tm.number_of_patches == 1 else [2]
+        for kind in kinds:
+            check(lib.ytm_compile_train_kernel(ctypes.byref(params), kind, int(bool(injected))))
+        return kinds
+
     def _gpu_init(self) -> None:
+        if getattr(self, "_skip_gpu_init", False):
+            self._handle = None
+            return
         self._params_c = self._params()
         handle = ctypes.c_void_p()
         check(lib.ytm_create(ctypes.byref(self._params_c), ctypes.byref(handle)))

@@ -224,6 +224,21 @@ void ytm_destroy(ytm_model* m) {
   delete m;
 }
 
+int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injected) {
+  if (!params) return fail(YTM_EINVAL, "null params");
+  if (train_kind < 0 || train_kind > 2) return fail(YTM_EINVAL, "train_kind must be 0, 1 or 2");
+  Geom g;
+  int rc = resolve_geometry(*params, &g);
+  if (rc) return rc;
+  if ((g.P == 1) != (train_kind != 2))
+    return fail(YTM_EINVAL, "train_kind 2 is for several patches, 0 and 1 for one patch");
+  std::vector<char> code;
+  std::string why;
+  if (!ytm::jit_compile(g, (ytm::TrainKind)train_kind, injected != 0, &code, &why))
+    return fail(YTM_EHIP, why);
+  return YTM_OK;
+}
+
 int ytm_geometry(const ytm_model* m, int64_t out[4]) {
   if (!m || !out) return fail(YTM_EINVAL, "null argument");
   out[0] = m->g.L;
@@ -330,8 +345,21 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     kind = ytm::TrainKind::kResident;
   const int rng_slots = kind == ytm::TrainKind::kResident ? ytm::train_rng_slots(cpw, g) : 0;
   const size_t lds = ytm::train_lds_bytes(kind, cpw, rng_slots, g);
+  // Kernel specialised for this model's geometry (hipRTC), else the built-in one.
+  // YTM_JIT=0 selects the built-in kernel; YTM_JIT=2 makes an unavailable compile an error.
+  hipFunction_t jit_fn = nullptr;
+  if (ytm::jit_enabled()) {
+    std::string why;
+    jit_fn = ytm::jit_train_kernel(g, kind, inj, &why);
+    const char* jit_env = std::getenv("YTM_JIT");
+    if (!jit_fn && jit_env && std::atoi(jit_env) == 2)
+      return fail(YTM_EHIP, "specialised training kernel unavailable: " + why);
+  }
   int bpc = 0;
-  HIP_TRY(ytm::train_occupancy(kind, inj, lds, &bpc));
+  if (jit_fn)
+    HIP_TRY(ytm::jit_occupancy(jit_fn, lds, &bpc));
+  else
+    HIP_TRY(ytm::train_occupancy(kind, inj, lds, &bpc));
   if ((int64_t)bpc * m->cus < grid)
     return fail(YTM_EINVAL, "training grid does not fit co-resident on the device");
   m->stats.train_workgroups = grid;
@@ -412,7 +440,10 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.profile = prof_env && std::atoi(prof_env) > 0;
     a.g = g;
     FIT_TRY(hipEventRecord(m->ev0, m->stream));
-    FIT_TRY(ytm::launch_train(a, grid, lds, kind, inj, m->stream));
+    if (jit_fn)
+      FIT_TRY(ytm::launch_train_jit(jit_fn, a, grid, lds, m->stream));
+    else
+      FIT_TRY(ytm::launch_train(a, grid, lds, kind, inj, m->stream));
     FIT_TRY(hipEventRecord(m->ev1, m->stream));
     FIT_TRY(hipEventSynchronize(m->ev1));
     float ms = 0.0f;
@@ -435,6 +466,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
 #undef FIT_TRY
   m->stats.last_fit_wait_frac = cnt[2] ? (double)cnt[1] / (double)cnt[2] : 0.0;
   m->stats.train_kind = (int32_t)kind;
+  m->stats.train_specialised = jit_fn != nullptr;
   m->stats.step += (uint64_t)count;
   m->stats.last_fit_samples = (uint64_t)count;
   m->stats.last_fit_updates = upd;

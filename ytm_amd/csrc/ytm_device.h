@@ -8,8 +8,7 @@
 //    is exactly "plane NP-1 set": the include mask of a clause is its top plane.
 //  * wave64 helpers.
 #pragma once
-#include <hip/hip_runtime.h>
-#include <stdint.h>
+#include "ytm_types.h"
 
 namespace ytm {
 

@@ -1,0 +1,718 @@
+// ytm_train.h -- device code of the YTM training kernels (gfx950).
+//
+// Included by the built-in kernels (ytm_kernels.hip) with the model geometry read from
+// the kernel arguments, and compiled again at run time by hipRTC (ytm_jit.hip) with the
+// geometry as a constexpr Geom, so that every size and hyperparameter folds to a
+// constant.  Every function takes the geometry as `const Geom& g`.
+#pragma once
+#include "ytm_device.h"
+#include "ytm_types.h"
+
+namespace ytm {
+
+// ========================================================================= training
+// Persistent, cooperative kernel: one launch trains N consecutive samples.
+// Workgroup b owns clauses [C*b/G, C*(b+1)/G) for the whole launch.  Per sample:
+//   A. each wave takes own clauses: include mask (top plane) vs the sample, all patches
+//      (fast_eval, kernel.cu:255-282), reservoir choice of the firing patch
+//      (select_active, kernel.cu:285-316), patch weight, partial class sums in LDS;
+//   B. the workgroup adds (1<<44 | partial) into its copy of the sample's class-sum
+//      slots (agent-scope atomics; copies keep contention to ~16 workgroups per word),
+//      then waits until every copy holds its full workgroup count;
+//   C. clip / target / update probability per class (kernel.cu:397,508-529,543-551);
+//   D. feedback on own clauses (clause_update, kernel.cu:531-613): per class in order,
+//      Q-skip and update draws, Type Ia / Ib / II, weight update, and the literal updates
+//      applied bit-sliced to the clause's planes, 32 literals per lane.
+// The only cross-workgroup traffic is the K class sums of each sample.
+
+// Bounded wait for the class sums: at most kWaitTicks of the 100 MHz real-time counter
+// (2 s), independent of how long one poll takes under contention.
+constexpr uint64_t kWaitTicks = 200000000ull;
+
+// Plane groups (4 planes each, most significant first) of the literal draws that the
+// resident kernel computes cooperatively ahead of applying an update.
+constexpr int kPreGroups = 3;
+
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int t = __shfl_up(v, off);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
+// Literal-decrement mask of one (clause, class) update for the 32 literals of word w:
+// bit b set iff need bit b is set and u(literal 32w+b) <= S_INV.
+template <bool INJECT>
+__device__ __forceinline__ uint32_t literal_draw_mask(const TrainArgs& a, const Geom& g, const float* inj, uint32_t need,
+                                                      uint64_t t, int64_t c, int64_t k, int64_t w,
+                                                      const uint32_t* pre, bool have_pre) {
+  if (INJECT) {
+    uint32_t res = 0u;
+    if (need) {
+      const float* u = inj + g.C * g.P + 2 * g.C * g.K + (c * g.K + k) * g.L + w * 32;
+      for (int b = 0; b < 32; ++b)
+        if (((need >> b) & 1u) && (double)u[b] <= g.s_inv) res |= 1u << b;
+    }
+    return res;
+  } else {
+    // u <= S_INV  <=>  q < s_thr for the 24-bit integer q of the literal; decided from the
+    // most significant plane down, 4 planes per Philox call, until no lane of the wave
+    // has an undecided literal.
+    if (g.s_thr >= (1u << 24)) return need;
+    if (g.s_thr == 0u) return 0u;
+    uint32_t lt = 0u, eq = need;
+    for (int grp = 0; grp < 6; ++grp) {
+      if (!__any(eq != 0u)) break;
+      U4 z;
+      if (have_pre && grp < kPreGroups) {
+        // plane group computed ahead of time by the workgroup (zero words for idle lanes)
+        z = pre ? U4{pre[grp * 4 + 0], pre[grp * 4 + 1], pre[grp * 4 + 2], pre[grp * 4 + 3]} : U4{0u, 0u, 0u, 0u};
+      } else {
+        z = site_words(a.seed, t, (uint32_t)c, TAG_LIT, (uint32_t)((k * g.W + w) * 6 + grp));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 23 - 4 * grp - i;
+        const uint32_t pl = word_of(z, i);
+        if ((g.s_thr >> j) & 1u) {
+          lt |= eq & ~pl;
+          eq &= pl;
+        } else {
+          eq &= ~pl;
+        }
+      }
+    }
+    return lt;
+  }
+}
+
+// Phase A for one clause (wave-uniform): returns the selected patch or -1 and the
+// clause's include count.  m: the clause's include mask (W words), xe: the sample (P*W).
+template <bool VANILLA, bool INJECT, bool PRE = false>
+__device__ int eval_select(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, const uint32_t* m,
+                           const uint32_t* xe, bool dropped, float u_pre, int* ninc_out) {
+  const int lane = lane_id();
+  // The include count only matters through "empty" and "<= MAX_INCLUDED_LITERALS"; when
+  // that bound is at least L, a 0/1 emptiness flag stands in for it.
+  const bool exact_count = g.maxinc < g.L;
+  if (VANILLA) {
+    uint32_t bad = 0u, any = 0u;
+    int cnt = 0;
+    for (int64_t w = lane; w < g.W; w += kWave) {
+      const uint32_t mw = m[w];
+      if (exact_count) cnt += __popc(mw);
+      any |= mw;
+      bad |= mw & ~xe[w];
+    }
+    const int ninc = exact_count ? wave_sum_i32(cnt) : (__any(any != 0u) ? 1 : 0);
+    *ninc_out = ninc;
+    const bool any_bad = __any(bad != 0u);
+    if (dropped) return -1;
+    if (ninc != 0 && any_bad) return -1;
+    // One firing patch: its draw must be below 1.0f / 1.
+    float u;
+    if (INJECT)
+      u = inj[c * g.P];
+    else if (PRE)
+      u = u_pre;
+    else
+      u = uniform_from_word(site_words(a.seed, t, (uint32_t)c, TAG_SEL, 0u).x);
+    return u < 1.0f ? 0 : -1;  // 1.0f / 1
+  } else {
+    int cnt = 0;
+    uint32_t any = 0u;
+    for (int64_t w = lane; w < g.W; w += kWave) {
+      const uint32_t mw = m[w];
+      if (exact_count) cnt += __popc(mw);
+      any |= mw;
+    }
+    const int ninc = exact_count ? wave_sum_i32(cnt) : (__any(any != 0u) ? 1 : 0);
+    *ninc_out = ninc;
+    if (dropped) return -1;
+    // Firing bitmap: lane q keeps bits of patches [64q, 64q+64).
+    unsigned long long myfire = 0ull;
+    int R = 0;
+    const int nch = (int)((g.P + kWave - 1) / kWave);
+    for (int ch = 0; ch < nch; ++ch) {
+      const int64_t p = (int64_t)ch * kWave + lane;
+      bool ok = p < g.P;
+      if (ok && ninc != 0) {
+        const uint32_t* xp = xe + p * g.W;
+        for (int64_t w = 0; w < g.W; ++w)
+          if (m[w] & ~xp[w]) {
+            ok = false;
+            break;
+          }
+      }
+      const unsigned long long b = __ballot(ok);
+      if (lane == ch) myfire = b;
+      R += __popcll(b);
+    }
+    if (R == 0) return -1;
+    // Reservoir: the selected firing patch is the one of highest rank r whose draw is
+    // below 1.0f / r; scan ranks from R downward, 256 ranks (64 Philox calls) at a time.
+    int best = 0;
+    for (int g0 = (R - 1) >> 2; g0 >= 0; g0 -= kWave) {
+      const int gl = g0 - lane;
+      int lb = 0;
+      if (gl >= 0) {
+        if (INJECT) {
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * gl + 1 + j;
+            if (r <= R && inj[c * g.P + (r - 1)] < a.inv_rank[r]) lb = r;
+          }
+        } else {
+          const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * gl + 1 + j;
+            if (r <= R && uniform_from_word(word_of(z, j)) < a.inv_rank[r]) lb = r;
+          }
+        }
+      }
+      best = wave_max_i32(lb);
+      if (best > 0) break;
+    }
+    if (best == 0) return -1;
+    // Patch of the best-th set bit of the firing bitmap.
+    const int pc = lane < nch ? __popcll(myfire) : 0;
+    const int incl = wave_inclusive_scan(pc);
+    const int excl = incl - pc;
+    const bool here = lane < nch && best > excl && best <= incl;
+    const unsigned long long hb = __ballot(here);
+    const int src = __ffsll((long long)hb) - 1;
+    int pos = 0;
+    if (lane == src) {
+      unsigned long long v = myfire;
+      for (int q = 1; q < best - excl; ++q) v &= v - 1ull;
+      pos = src * kWave + __ffsll((long long)v) - 1;
+    }
+    return __shfl(pos, src);
+  }
+}
+
+struct FbOps {
+  unsigned long long m1a, m1b, m2;  // bit k - kb: class k runs Type Ia / Ib / II
+};
+
+// Phase D decisions for one non-dropped clause (clause_update, kernel.cu:567-610): per
+// class, the Q-skip and update draws, the feedback type, and the weight update.  The
+// literal updates are left to apply_ops.  Wave-uniform result.
+template <bool INJECT, bool PRE = false>
+__device__ FbOps decide(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, int sel, int ninc,
+                        const int* s_tgt, const double* s_prob, float* wrow, const float* pre_uq,
+                        const float* pre_uu) {
+  const int lane = lane_id();
+  const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+  const int kn = g.coalesced ? (int)g.K : 1;
+  const bool o = sel >= 0;
+  const bool small = o && ninc <= g.maxinc;
+  int type = 0;
+  if (lane < kn) {
+    const int64_t k = kb + lane;
+    const int tgt = s_tgt[k];
+    float uq, uu;
+    if (INJECT) {
+      uq = inj[g.C * g.P + c * g.K + k];
+      uu = inj[g.C * g.P + g.C * g.K + c * g.K + k];
+    } else if (PRE) {
+      uq = pre_uq[k];
+      uu = pre_uu[k];
+    } else {
+      const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)k);
+      uq = uniform_from_word(z.x);
+      uu = uniform_from_word(z.y);
+    }
+    const bool skip = tgt == -1 && (double)uq > g.q_prob;
+    if (!skip) {
+      float* wp = wrow + k;
+      float wv = *wp;
+      const int sign = (wv >= 0.0f) - (wv < 0.0f);
+      const bool upd = (double)uu <= s_prob[k];
+      const int ts = tgt * sign;
+      if (upd) {
+        if (ts > 0 && small) {
+          wv += (float)sign * 1.0f;
+          *wp = wv;
+          type = 1;
+        } else if (ts > 0) {
+          type = 2;
+        } else if (ts < 0 && o) {
+          wv -= (float)sign * 1.0f;
+          if (!g.negative_polarity && wv < 1.0f) wv = 1.0f;
+          *wp = wv;
+          type = 3;
+        }
+      }
+    }
+  }
+  return FbOps{__ballot(type == 1), __ballot(type == 2), __ballot(type == 3)};
+}
+
+// Literal updates of one clause for the feedback decided in ops, applied class by class
+// in increasing k to the clause's planes (cplanes, stride W).  pre, when given, holds the
+// first kPreGroups plane groups of the literal draws of every Type Ia/Ib class, in the
+// order of those classes: [op][W][kPreGroups][4].
+template <bool INJECT>
+__device__ void apply_ops(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, int sel, FbOps ops,
+                          uint32_t* cplanes, const uint32_t* xe, const uint32_t* pre) {
+  const int lane = lane_id();
+  const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+  const bool o = sel >= 0;
+  const uint32_t* xsel = o ? xe + (int64_t)sel * g.W : nullptr;
+  const int np = g.np;
+  const unsigned long long all = ops.m1a | ops.m1b | ops.m2;
+  for (int64_t wb = 0; wb < g.W; wb += kWave) {
+    const int64_t w = wb + lane;
+    const bool act = w < g.W;
+    const uint32_t F = act ? (w == g.W - 1 ? g.last_filter : 0xFFFFFFFFu) : 0u;
+    uint32_t* pw = cplanes + w;
+    uint32_t pl[kMaxPlanes];
+#pragma unroll
+    for (int j = 0; j < kMaxPlanes; ++j) pl[j] = (j < np && act) ? pw[(int64_t)j * g.W] : 0u;
+    const uint32_t xb = (o && act) ? xsel[w] : 0u;
+    unsigned long long rem = all;
+    int rng_op = 0;
+    while (rem) {
+      const int b = __ffsll((long long)rem) - 1;
+      rem &= rem - 1ull;
+      const int64_t k = kb + b;
+      if (((ops.m1a | ops.m1b) >> b) & 1ull) {
+        // Type Ia (kernel.cu:410-443): literal 1 -> +1 below MAX, literal 0 -> -1 w.p. 1/s.
+        // Type Ib (kernel.cu:453-470): every literal -1 w.p. 1/s.
+        const bool t1a = (ops.m1a >> b) & 1ull;
+        const uint32_t pos = planes_gt(pl, np, g.off) & F;
+        const uint32_t need = t1a ? (~xb & pos) : pos;
+        const uint32_t* pre_w = (pre && act) ? pre + ((int64_t)rng_op * g.W + w) * (kPreGroups * 4) : nullptr;
+        const uint32_t dec = literal_draw_mask<INJECT>(a, g, inj, need, t, c, k, w, pre_w, pre != nullptr);
+        if (t1a) planes_inc(pl, np, xb & planes_lt(pl, np, g.max_state_p) & F);
+        planes_dec(pl, np, dec);
+        ++rng_op;
+      } else {
+        // Type II (kernel.cu:481-506): literal 0 -> +1, no upper guard.
+        planes_inc(pl, np, ~xb & F);
+      }
+    }
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < kMaxPlanes; ++j)
+        if (j < np) pw[(int64_t)j * g.W] = pl[j];
+    }
+  }
+}
+
+// Phase D for one non-dropped clause.  Returns true when any Type Ia/Ib/II branch ran.
+// cplanes: the clause's np planes (stride W), wrow: its K weights, xe: the sample.
+template <bool INJECT>
+__device__ bool feedback(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, int sel, int ninc,
+                         const int* s_tgt, const double* s_prob, uint32_t* cplanes, float* wrow,
+                         const uint32_t* xe, const float* pre_uq, const float* pre_uu) {
+  const FbOps ops = decide<INJECT, false>(a, g, inj, c, t, sel, ninc, s_tgt, s_prob, wrow, pre_uq, pre_uu);
+  if ((ops.m1a | ops.m1b | ops.m2) == 0ull) return false;
+  apply_ops<INJECT>(a, g, inj, c, t, sel, ops, cplanes, xe, nullptr);
+  return true;
+}
+
+// Phases B and C, run by wave 0 of every workgroup.  Per sample, a two-level all-reduce
+// of the K class sums with a broadcast back:
+//   1. lanes < K add (1<<44 | partial) into their group's word (groups of S workgroups);
+//   2. for each word, the adder that completes its group (returned count == group size)
+//      forwards the group total into the final word;
+//   3. for each word, the forwarder that completes the final word (count == groups)
+//      stores the total into every group's mailbox;
+//   4. each workgroup polls its own group's mailbox (bounded in real time).
+// Contention stays at <= S adders / pollers per word.  With one group the group words are
+// polled directly.  Lanes < K then derive clip / target / update probability
+// (kernel.cu:397,508-529,543-551).  Returns false when the wait expired.
+__device__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, const int32_t* y_row, const float* bias,
+                                    long long* s_part, int* s_tgt, double* s_prob, int* s_abort,
+                                    uint64_t* wait_ticks) {
+  const int lane = lane_id();
+  const int G = gridDim.x, wg = blockIdx.x;
+  const int d = wg / a.S;
+  const unsigned long long gsize = (unsigned long long)min(a.S, G - d * a.S);
+  const int ks = ((int)g.K + 15) & ~15;                    // words per row (128-byte multiples)
+  unsigned long long* row = a.slots + (int64_t)i * a.slot_stride;
+  unsigned long long* group_w = row;                       // [D][ks]
+  unsigned long long* final_w = row + a.D * ks;            // [ks]
+  unsigned long long* mbox = final_w + ks;                 // [D][ks]
+  unsigned long long* poll = a.D == 1 ? group_w : mbox + d * ks;
+  const unsigned long long poll_count = a.D == 1 ? gsize : (unsigned long long)a.D;
+  if (lane < g.K) {
+    const long long part = s_part[lane];
+    s_part[lane] = 0;
+    const unsigned long long mine = (1ull << 44) + (unsigned long long)part;
+    if (a.D == 1) {
+      __hip_atomic_fetch_add(&group_w[lane], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      const unsigned long long now =
+          __hip_atomic_fetch_add(&group_w[d * ks + lane], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+      if (((now + (1ull << 43)) >> 44) == gsize) {
+        const unsigned long long fwd = (1ull << 44) + (now - (gsize << 44));
+        const unsigned long long now2 =
+            __hip_atomic_fetch_add(&final_w[lane], fwd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + fwd;
+        if (((now2 + (1ull << 43)) >> 44) == (unsigned long long)a.D)
+          for (int m = 0; m < a.D; ++m)
+            __hip_atomic_store(&mbox[m * ks + lane], now2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+  unsigned long long v = 0;
+  for (;;) {
+    bool ok = true;
+    if (lane < g.K) {
+      v = __hip_atomic_load(&poll[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = ((v + (1ull << 43)) >> 44) == poll_count;
+    }
+    if (__all(ok)) break;
+    if (__builtin_amdgcn_s_memrealtime() - t_start > kWaitTicks) {
+      // Record the first stall: err = {1, sample, workgroup, count seen by lane 0}.
+      if (lane == 0) {
+        *s_abort = 1;
+        if (atomicCAS(a.err, 0, 1) == 0) {
+          a.err[1] = i;
+          a.err[2] = wg;
+          a.err[3] = (int)((v + (1ull << 43)) >> 44);
+        }
+      }
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  *wait_ticks += __builtin_amdgcn_s_memrealtime() - t_start;
+  if (lane < g.K) {
+    const int k = lane;
+    const long long S = (long long)(v - (poll_count << 44)) + (long long)bias[k];
+    const float cs = (float)S;
+    const float vclip = ((double)cs > g.thresh) ? (float)g.thresh : (((double)cs < -g.thresh) ? (float)(-g.thresh) : cs);
+    const int y = y_row[k];
+    s_tgt[k] = 1 - 2 * (vclip > (float)y);
+    s_prob[k] = ((double)y - (double)vclip) / (2.0 * (double)y);
+  }
+  return true;
+}
+
+__device__ __forceinline__ void add_partial(const TrainArgs& a, const Geom& g, long long* s_part, int64_t c, const float* wrow) {
+  const int lane = lane_id();
+  if (g.coalesced) {
+    if (lane < g.K) atomicAdd((unsigned long long*)&s_part[lane], (unsigned long long)(long long)wrow[lane]);
+  } else if (lane == 0) {
+    const int64_t k = c / g.per_bank;
+    atomicAdd((unsigned long long*)&s_part[k], (unsigned long long)(long long)wrow[k]);
+  }
+}
+
+// Clause state in global memory (L2/MALL resident across samples); any P.
+template <bool VANILLA, bool INJECT>
+__device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom& g) {
+  extern __shared__ long long dyn_lds[];
+  __shared__ long long s_part[64];
+  __shared__ int s_tgt[64];
+  __shared__ double s_prob[64];
+  __shared__ int s_next;
+  __shared__ int s_abort;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int G = gridDim.x, wg = blockIdx.x;
+  const int64_t c_begin = g.C * wg / G, c_end = g.C * (wg + 1) / G;
+  const int n_own = (int)(c_end - c_begin);
+  int* s_sel = (int*)dyn_lds;                          // [cpw]
+  int* s_ninc = s_sel + a.cpw;                         // [cpw]
+  unsigned long long my_updates = 0ull;
+  uint64_t wait_ticks = 0;
+  const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
+  if (threadIdx.x == 0) s_abort = 0;
+
+  for (int i = 0; i < a.N; ++i) {
+    const uint64_t t = a.step0 + (uint64_t)i;
+    const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
+    const uint32_t* xe = a.X + (int64_t)i * g.P * g.W;
+    if (threadIdx.x == 0) s_next = 0;
+    __syncthreads();
+
+    // ---- A: evaluation, reservoir selection, partial class sums
+    for (;;) {
+      int idx = 0;
+      if (lane == 0) idx = atomicAdd(&s_next, 1);
+      idx = __shfl(idx, 0);
+      if (idx >= n_own) break;
+      const int64_t c = c_begin + idx;
+      int ninc;
+      const int sel = eval_select<VANILLA, INJECT>(a, g, inj, c, t, a.planes + (c * g.np + g.np - 1) * g.W, xe,
+                                                   a.drop[c] == 1u, -1.0f, &ninc);
+      if (lane == 0) {
+        s_sel[idx] = sel;
+        s_ninc[idx] = ninc;
+      }
+      if (sel >= 0) {
+        if (lane == 0) a.patch_w[c * g.P + sel] += 1;
+        add_partial(a, g, s_part, c, a.weights + c * g.K);
+      }
+    }
+    __syncthreads();
+
+    // ---- B + C
+    if (wave == 0)
+      exchange_class_sums(a, g, i, a.Y + (int64_t)i * g.K, a.bias, s_part, s_tgt, s_prob, &s_abort, &wait_ticks);
+    if (threadIdx.x == 0) s_next = 0;
+    __syncthreads();
+    if (s_abort) break;
+
+    // ---- D: feedback
+    for (;;) {
+      int idx = 0;
+      if (lane == 0) idx = atomicAdd(&s_next, 1);
+      idx = __shfl(idx, 0);
+      if (idx >= n_own) break;
+      const int64_t c = c_begin + idx;
+      if (a.drop[c] == 1u) continue;
+      const bool touched = feedback<INJECT>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob,
+                                            a.planes + c * g.np * g.W, a.weights + c * g.K, xe, nullptr, nullptr);
+      if (touched && lane == 0) ++my_updates;
+    }
+    __syncthreads();
+  }
+  if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
+  if (threadIdx.x == 0) {
+    atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
+    atomicAdd(&a.counters[2], (unsigned long long)(__builtin_amdgcn_s_memrealtime() - t_kernel));
+  }
+}
+
+// Copies sample i (its literal words and its K targets) into LDS buffer i & 1, threads
+// [first, first + count) of the workgroup taking part.
+__device__ __forceinline__ void stage_sample(const TrainArgs& a, const Geom& g, int i, uint32_t* s_x, int32_t* s_y, int first,
+                                             int count) {
+  for (int64_t j = first; j < g.W; j += count) s_x[(i & 1) * g.W + j] = a.X[(int64_t)i * g.W + j];
+  for (int64_t j = first; j < g.K; j += count) s_y[(i & 1) * g.K + j] = a.Y[(int64_t)i * g.K + j];
+}
+
+// Counter-stream draws of sample i for the workgroup's clauses, computed ahead of use:
+// the reservoir draw of rank 1 (s_usel[idx]) and the Q-skip / update draws
+// (s_uq / s_uu [i & 1][idx][k]).  Threads [first, first + count) take part.
+__device__ __forceinline__ void precompute_draws(const TrainArgs& a, const Geom& g, int i, int64_t c_begin, int n_own, float* s_usel,
+                                                 float* s_uq, float* s_uu, int first, int count) {
+  const uint64_t t = a.step0 + (uint64_t)i;
+  const int kn = g.coalesced ? (int)g.K : 1;
+  const int per = kn + 1;
+  for (int j = first; j < n_own * per; j += count) {
+    const int idx = j / per, r = j % per;
+    const int64_t c = c_begin + idx;
+    if (r == kn) {
+      s_usel[idx] = uniform_from_word(site_words(a.seed, t, (uint32_t)c, TAG_SEL, 0u).x);
+    } else {
+      const int64_t k = (g.coalesced ? 0 : c / g.per_bank) + r;
+      const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)k);
+      s_uq[((i & 1) * a.cpw + idx) * g.K + k] = uniform_from_word(z.x);
+      s_uu[((i & 1) * a.cpw + idx) * g.K + k] = uniform_from_word(z.y);
+    }
+  }
+}
+
+// Vanilla TM (one patch) with each workgroup's clause state resident in LDS for the
+// whole launch: planes [own][np][W] and weights [own][K] are loaded once, updated in
+// place and written back at the end.  While wave 0 exchanges the class sums of sample i,
+// the other waves stage sample i+1 (literals and targets) in the second LDS buffer and
+// compute its counter-stream draws.  Each wave owns a fixed subset of the workgroup's
+// clauses for both phases, so two workgroup barriers per sample suffice.
+template <bool INJECT>
+__device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Geom& g) {
+  extern __shared__ long long dyn_lds[];
+  __shared__ long long s_part[64];
+  __shared__ int s_tgt[64];
+  __shared__ double s_prob[64];
+  __shared__ int s_abort;
+  __shared__ int s_ntask, s_nslot;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int nwv = blockDim.x / kWave;
+  const int G = gridDim.x, wg = blockIdx.x;
+  const int64_t c_begin = g.C * wg / G, c_end = g.C * (wg + 1) / G;
+  const int n_own = (int)(c_end - c_begin);
+  const int64_t cw = (int64_t)g.np * g.W;  // plane words per clause
+  const int R = a.rng_slots;
+  unsigned long long* s_task_m = (unsigned long long*)dyn_lds;    // [cpw][3] feedback masks
+  uint32_t* s_planes = (uint32_t*)(s_task_m + 3 * a.cpw);         // [cpw][np][W]
+  float* s_w = (float*)(s_planes + a.cpw * cw);                   // [cpw][K]
+  uint32_t* s_x = (uint32_t*)(s_w + a.cpw * g.K);                 // [2][W]
+  int* s_sel = (int*)(s_x + 2 * g.W);                             // [cpw]
+  int* s_ninc = s_sel + a.cpw;                                    // [cpw]
+  int* s_drop = s_ninc + a.cpw;                                   // [cpw]
+  int32_t* s_y = s_drop + a.cpw;                                  // [2][K]
+  float* s_bias = (float*)(s_y + 2 * g.K);                        // [K]
+  float* s_usel = s_bias + g.K;                                   // [cpw]
+  float* s_uq = s_usel + a.cpw;                                   // [2][cpw][K]
+  float* s_uu = s_uq + 2 * a.cpw * g.K;                           // [2][cpw][K]
+  int* s_task_idx = (int*)(s_uu + 2 * a.cpw * g.K);               // [cpw]
+  int* s_task_sb = s_task_idx + a.cpw;                            // [cpw] first draw slot
+  int* s_slot_idx = s_task_sb + a.cpw;                            // [R] clause of a draw slot
+  int* s_slot_k = s_slot_idx + R;                                 // [R] class of a draw slot
+  uint32_t* s_rng = (uint32_t*)(s_slot_k + R);                    // [R][W][kPreGroups][4]
+  unsigned long long my_updates = 0ull;
+  uint64_t wait_ticks = 0;
+  const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
+  // Optional phase timing (wave 0's view, 100 MHz real-time counter).
+  const bool prof = a.profile && wave == 0;
+  uint64_t prof_acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint64_t prof_last = 0;
+#define YTM_PROF_MARK(j)                                      \
+  if (prof) {                                                 \
+    const uint64_t now_ = __builtin_amdgcn_s_memrealtime();   \
+    prof_acc[j] += now_ - prof_last;                          \
+    prof_last = now_;                                         \
+  }
+
+  for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) s_planes[j] = a.planes[c_begin * cw + j];
+  for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) s_w[j] = a.weights[c_begin * g.K + j];
+  for (int64_t j = threadIdx.x; j < n_own; j += blockDim.x) s_drop[j] = a.drop[c_begin + j] == 1u;
+  for (int64_t j = threadIdx.x; j < g.K; j += blockDim.x) s_bias[j] = a.bias[j];
+  stage_sample(a, g, 0, s_x, s_y, threadIdx.x, blockDim.x);
+  if (!INJECT) precompute_draws(a, g, 0, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x, blockDim.x);
+  if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
+  if (threadIdx.x == 0) {
+    s_abort = 0;
+    s_ntask = 0;
+    s_nslot = 0;
+  }
+  __syncthreads();
+  prof_last = __builtin_amdgcn_s_memrealtime();
+
+  for (int i = 0; i < a.N; ++i) {
+    const uint64_t t = a.step0 + (uint64_t)i;
+    const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
+    const uint32_t* xe = s_x + (i & 1) * g.W;
+
+    // ---- A
+    for (int idx = wave; idx < n_own; idx += nwv) {
+      const int64_t c = c_begin + idx;
+      int ninc;
+      const int sel = eval_select<true, INJECT, !INJECT>(a, g, inj, c, t, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W,
+                                                         xe, s_drop[idx] != 0, INJECT ? -1.0f : s_usel[idx], &ninc);
+      if (lane == 0) {
+        s_sel[idx] = sel;
+        s_ninc[idx] = ninc;
+      }
+      if (sel >= 0) {
+        if (lane == 0) atomicAdd(&a.patch_w[c], 1);
+        add_partial(a, g, s_part, c, s_w + idx * g.K);
+      }
+    }
+    YTM_PROF_MARK(0);
+    __syncthreads();
+    YTM_PROF_MARK(1);
+
+    // ---- B + C on wave 0; the other waves stage sample i+1 and its draws
+    const bool more = i + 1 < a.N;
+    if (wave == 0) {
+      if (lane == 0) {
+        s_ntask = 0;
+        s_nslot = 0;
+      }
+      exchange_class_sums(a, g, i, s_y + (i & 1) * g.K, s_bias, s_part, s_tgt, s_prob, &s_abort, &wait_ticks);
+      YTM_PROF_MARK(2);
+      if (nwv == 1 && more) {
+        stage_sample(a, g, i + 1, s_x, s_y, lane, kWave);
+        if (!INJECT) precompute_draws(a, g, i + 1, c_begin, n_own, s_usel, s_uq, s_uu, lane, kWave);
+      }
+    } else if (more) {
+      stage_sample(a, g, i + 1, s_x, s_y, threadIdx.x - kWave, blockDim.x - kWave);
+      if (!INJECT)
+        precompute_draws(a, g, i + 1, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x - kWave, blockDim.x - kWave);
+    }
+    __syncthreads();
+    YTM_PROF_MARK(3);
+    if (s_abort) break;
+
+    // ---- D (no barrier after it: the next phase A of a wave touches only that wave's
+    // own clauses, and every shared buffer it reads was written before a barrier of
+    // this sample)
+    if (INJECT) {
+      for (int idx = wave; idx < n_own; idx += nwv) {
+        if (s_drop[idx]) continue;
+        const bool touched = feedback<INJECT>(a, g, inj, c_begin + idx, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob,
+                                              s_planes + idx * cw, s_w + idx * g.K, xe, nullptr, nullptr);
+        if (touched && lane == 0) ++my_updates;
+      }
+      continue;
+    }
+    // D1: each wave decides its clauses' feedback and queues the ones with updates
+    for (int idx = wave; idx < n_own; idx += nwv) {
+      if (s_drop[idx]) continue;
+      const int64_t c = c_begin + idx;
+      const FbOps ops = decide<INJECT, true>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob, s_w + idx * g.K,
+                                       s_uq + ((i & 1) * a.cpw + idx) * g.K, s_uu + ((i & 1) * a.cpw + idx) * g.K);
+      if ((ops.m1a | ops.m1b | ops.m2) != 0ull && lane == 0) {
+        ++my_updates;
+        const unsigned long long rng = ops.m1a | ops.m1b;
+        const int tk = atomicAdd(&s_ntask, 1);
+        const int sb = atomicAdd(&s_nslot, __popcll(rng));
+        s_task_idx[tk] = idx;
+        s_task_sb[tk] = sb;
+        s_task_m[tk * 3 + 0] = ops.m1a;
+        s_task_m[tk * 3 + 1] = ops.m1b;
+        s_task_m[tk * 3 + 2] = ops.m2;
+        const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+        int j = sb;
+        for (unsigned long long r = rng; r; r &= r - 1ull, ++j) {
+          if (j < R) {
+            s_slot_idx[j] = idx;
+            s_slot_k[j] = (int)(kb + __ffsll((long long)r) - 1);
+          }
+        }
+      }
+    }
+    YTM_PROF_MARK(4);
+    __syncthreads();
+    YTM_PROF_MARK(5);
+    const int ntask = s_ntask;
+    if (ntask == 0) continue;
+    // D2: the whole workgroup computes the leading plane groups of every queued draw
+    const int nslot = min(s_nslot, R);
+    const int per_slot = (int)g.W * kPreGroups;
+    for (int item = threadIdx.x; item < nslot * per_slot; item += blockDim.x) {
+      const int sl = item / per_slot, rem = item % per_slot;
+      const int64_t w = rem / kPreGroups;
+      const int grp = rem % kPreGroups;
+      const int64_t k = s_slot_k[sl];
+      const U4 z = site_words(a.seed, t, (uint32_t)(c_begin + s_slot_idx[sl]), TAG_LIT,
+                              (uint32_t)((k * g.W + w) * 6 + grp));
+      uint32_t* dst = s_rng + ((int64_t)sl * g.W + w) * (kPreGroups * 4) + grp * 4;
+      dst[0] = z.x;
+      dst[1] = z.y;
+      dst[2] = z.z;
+      dst[3] = z.w;
+    }
+    __syncthreads();
+    YTM_PROF_MARK(6);
+    // D3: the owning wave applies each queued update
+    for (int tk = 0; tk < ntask; ++tk) {
+      const int idx = s_task_idx[tk];
+      if (idx % nwv != wave) continue;
+      const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
+      const int sb = s_task_sb[tk];
+      const bool have = sb + __popcll(ops.m1a | ops.m1b) <= R;
+      apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[idx], ops, s_planes + idx * cw, xe,
+                        have ? s_rng + (int64_t)sb * g.W * (kPreGroups * 4) : nullptr);
+    }
+    YTM_PROF_MARK(7);
+  }
+#undef YTM_PROF_MARK
+  __syncthreads();
+  for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) a.planes[c_begin * cw + j] = s_planes[j];
+  for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) a.weights[c_begin * g.K + j] = s_w[j];
+  if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
+  if (threadIdx.x == 0) {
+    atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
+    atomicAdd(&a.counters[2], (unsigned long long)(__builtin_amdgcn_s_memrealtime() - t_kernel));
+    if (prof)
+      for (int j = 0; j < 8; ++j) atomicAdd(&a.counters[4 + j], (unsigned long long)prof_acc[j]);
+  }
+}
+
+
+}  // namespace ytm

@@ -1,0 +1,85 @@
+// ytm_types.h -- structures shared by host code, the built-in kernels and the kernels
+// specialised per model at run time (hipRTC compiles this header too).
+#pragma once
+#if !defined(__HIPCC_RTC__)
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#else
+// hipRTC's built-in preamble declares the fixed-width integer types in __hip_internal.
+using __hip_internal::int32_t;
+using __hip_internal::int64_t;
+using __hip_internal::uint32_t;
+using __hip_internal::uint64_t;
+#endif
+
+namespace ytm {
+
+constexpr int kTrainThreads = 512;
+constexpr int kMaxPlanesHost = 16;  // must equal kMaxPlanes of ytm_device.h
+
+// Resolved model geometry and hyperparameters.  Listed once (X-macro) so that host code
+// can print a constexpr initializer in declaration order for a specialised compile.
+#define YTM_GEOM_FIELDS(X)                                                                           \
+  X(int64_t, C)            /* clauses */                                                             \
+  X(int64_t, K)            /* classes */                                                             \
+  X(int64_t, L)            /* literals */                                                            \
+  X(int64_t, W)            /* literal words */                                                       \
+  X(int64_t, P)            /* patches */                                                             \
+  X(int64_t, Lh)           /* positive literals */                                                   \
+  X(int64_t, F)            /* input features per sample */                                           \
+  X(int, np)               /* TA bit-planes */                                                       \
+  X(uint32_t, off)         /* stored plane value s' = s + off */                                     \
+  X(uint32_t, max_state_p) /* number_of_ta_states + off */                                           \
+  X(uint32_t, last_filter) /* valid-literal mask of word W-1 (kernel.cu:36-40) */                    \
+  X(int, half_state)       /* number_of_ta_states / 2 */                                             \
+  X(int, max_state)        /* number_of_ta_states */                                                 \
+  X(int, per_bank)         /* clauses per bank (C when coalesced) */                                 \
+  X(int, dim0)                                                                                       \
+  X(int, dim1)                                                                                       \
+  X(int, dim2)                                                                                       \
+  X(int, pd0)                                                                                        \
+  X(int, pd1)                                                                                        \
+  X(int, append_negated)                                                                             \
+  X(int, encode_loc)                                                                                 \
+  X(int, coalesced)                                                                                  \
+  X(int, negative_polarity)                                                                          \
+  X(int, init_neg_weights)                                                                           \
+  X(int, maxinc)           /* MAX_INCLUDED_LITERALS */                                               \
+  X(double, thresh)        /* T */                                                                   \
+  X(double, s_inv)         /* typed S_INV widened to double */                                       \
+  X(double, q_prob)        /* typed Q_PROB widened to double */                                      \
+  X(uint32_t, s_thr)       /* floor(s_inv * 2^24) clamped to [0, 2^24] */
+
+struct Geom {
+#define YTM_GEOM_DECL(type, name) type name;
+  YTM_GEOM_FIELDS(YTM_GEOM_DECL)
+#undef YTM_GEOM_DECL
+};
+
+struct TrainArgs {
+  uint32_t* planes;          // [C][np][W]
+  float* weights;            // [C][K]
+  int32_t* patch_w;          // [C][P]
+  const float* bias;         // [K]
+  const uint32_t* X;         // [N][P][W]  (first sample of this launch)
+  const int32_t* Y;          // [N][K]
+  const uint32_t* drop;      // [C]
+  const float* inject;       // [N][inject_block] or nullptr
+  const float* inv_rank;     // [P + 1], inv_rank[r] = 1.0f / r
+  unsigned long long* slots; // [N][slot_stride], zero on entry
+  unsigned long long* counters;  // [0] updated clauses, [1] wait ticks, [2] kernel ticks, [4..11] phases
+  int* err;                  // {1, sample, workgroup, count} when a bounded wait expires
+  int64_t inject_block;
+  uint64_t step0;
+  uint64_t seed;
+  int N;
+  int S;                     // workgroups per class-sum group
+  int D;                     // class-sum groups (ceil(grid / S))
+  int64_t slot_stride;       // slot words per sample: D == 1 ? ks : (2D + 1) * ks, ks = K rounded up to 16
+  int cpw;                   // max clauses owned by one workgroup
+  int rng_slots;             // literal-draw slots precomputed per sample (resident kernel)
+  int profile;               // accumulate per-phase times into counters[4..11]
+  Geom g;
+};
+
+}  // namespace ytm
