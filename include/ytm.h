@@ -88,13 +88,15 @@ int ytm_get_stats(const ytm_model *m, ytm_stats *out);
 /* Reseed the random stream and reset its step to 0 (what re-running __init__ does). */
 int ytm_set_seed(ytm_model *m, uint64_t seed);
 /* Compile (and cache for this process) the training kernel specialised for the geometry
- * of *params, without touching a GPU.  train_kind as in ytm_stats (0 resident, 1 global
- * one patch, 2 global several patches); injected != 0 for the injected-draw variant.
+ * of *params and the launch shape used on a device with compute_units CUs (0: 256, an
+ * MI355X), without touching a GPU.  train_kind as in ytm_stats (0 resident, 1 global one
+ * patch, 2 global several patches); injected != 0 for the injected-draw variant.
  * The counterpart of the per-model kernel compile in BaseTM.__init__
  * (src/cutm/base.py:129-159); ytm_fit compiles on first use anyway, so calling this is
  * optional (warm-up, or checking that the compiler is available).  YTM_EHIP with the
  * compiler log in ytm_last_error() on failure. */
-int ytm_compile_train_kernel(const ytm_params *params, int train_kind, int injected);
+int ytm_compile_train_kernel(const ytm_params *params, int train_kind, int injected,
+                             int compute_units);
 
 /* encode: BaseTM.encode (src/cutm/base.py:224-263; kernel.cu:76-152 encode_batch).
  * X: uint32 (N, dim0*dim1*dim2), any value > 0 is a set pixel.  out: uint32 (N, P, W). */

@@ -75,9 +75,11 @@ def test_compile_entry_point_rejects_bad_kind():
     tm._skip_gpu_init = True
     tm.__init__(10, 15, 3.9, (12, 1, 1), 2, seed=1)
     params = tm._params()
-    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 2, 0) == 1  # several patches only
-    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 7, 0) == 1
+    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 2, 0, 0) == 1  # several patches only
+    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 7, 0, 0) == 1
     assert b"train_kind" in _lib.lib.ytm_last_error()
+    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 0, 0, -1) == 1
+    assert b"compute_units" in _lib.lib.ytm_last_error()
 
 
 @pytest.mark.parametrize(

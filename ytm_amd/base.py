@@ -182,18 +182,19 @@ class BaseTM:
         return p
 
     @classmethod
-    def compile_kernels(cls, *args, injected: bool = False, **kwargs) -> list[int]:
+    def compile_kernels(cls, *args, injected: bool = False, compute_units: int = 0, **kwargs) -> list[int]:
         """Compile and cache, for this process, the training kernels specialised for a model
-        built with these arguments; needs no GPU (the counterpart of the per-model compile
-        in the reference's BaseTM.__init__, src/cutm/base.py:129-159).  Fitting compiles on
-        first use anyway.  Returns the training-kernel kinds compiled."""
+        built with these arguments, for a device with `compute_units` CUs (0: an MI355X's
+        256); needs no GPU (the counterpart of the per-model compile in the reference's
+        BaseTM.__init__, src/cutm/base.py:129-159).  Fitting compiles on first use anyway.
+        Returns the training-kernel kinds compiled."""
         tm = cls.__new__(cls)
         tm._skip_gpu_init = True
         tm.__init__(*args, **kwargs)
         params = tm._params()
         kinds = [0, 1] if tm.number_of_patches == 1 else [2]
         for kind in kinds:
-            check(lib.ytm_compile_train_kernel(ctypes.byref(params), kind, int(bool(injected))))
+            check(lib.ytm_compile_train_kernel(ctypes.byref(params), kind, int(bool(injected)), int(compute_units)))
         return kinds
 
     def _gpu_init(self) -> None:

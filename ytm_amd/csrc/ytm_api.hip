@@ -144,17 +144,28 @@ constexpr size_t kResidentLdsLimit = 150 * 1024;
 
 // Picks the persistent grid (one workgroup per CU at most, at least ~8 clauses each) and
 // the class-sum grouping (groups of <= 16 workgroups).
-void train_shape(const ytm_model* m, int* grid, int* S, int* D, int* cpw) {
+void train_shape(int64_t C, int cus, int* grid, int* S, int* D, int* cpw) {
   const char* env = std::getenv("YTM_TRAIN_WGS");
-  int64_t G = std::min<int64_t>(m->cus, std::max<int64_t>(1, (m->g.C + 7) / 8));
-  if (env && std::atoi(env) > 0) G = std::min<int64_t>(std::atoi(env), m->g.C);
+  int64_t G = std::min<int64_t>(cus, std::max<int64_t>(1, (C + 7) / 8));
+  if (env && std::atoi(env) > 0) G = std::min<int64_t>(std::atoi(env), C);
   *grid = (int)G;
   const char* envs = std::getenv("YTM_TRAIN_GROUP");
   int s = envs && std::atoi(envs) > 0 ? std::atoi(envs) : 16;
   s = (int)std::min<int64_t>(s, G);
   *S = s;
   *D = (int)((G + s - 1) / s);
-  *cpw = (int)((m->g.C + G - 1) / G) + 1;
+  *cpw = (int)((C + G - 1) / G) + 1;
+}
+
+// The model geometry plus the launch shape of a training run on `cus` compute units.
+Geom train_geometry(const Geom& model, int cus, int* cpw) {
+  int grid, S, D;
+  train_shape(model.C, cus, &grid, &S, &D, cpw);
+  Geom g = model;
+  g.grid = grid;
+  g.group_size = S;
+  g.groups = D;
+  return g;
 }
 
 }  // namespace
@@ -224,12 +235,15 @@ void ytm_destroy(ytm_model* m) {
   delete m;
 }
 
-int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injected) {
+int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injected, int compute_units) {
   if (!params) return fail(YTM_EINVAL, "null params");
   if (train_kind < 0 || train_kind > 2) return fail(YTM_EINVAL, "train_kind must be 0, 1 or 2");
-  Geom g;
-  int rc = resolve_geometry(*params, &g);
+  if (compute_units < 0) return fail(YTM_EINVAL, "compute_units must be >= 0");
+  Geom model;
+  int rc = resolve_geometry(*params, &model);
   if (rc) return rc;
+  int cpw;
+  const Geom g = train_geometry(model, compute_units > 0 ? compute_units : 256, &cpw);
   if ((g.P == 1) != (train_kind != 2))
     return fail(YTM_EINVAL, "train_kind 2 is for several patches, 0 and 1 for one patch");
   std::vector<char> code;
@@ -333,9 +347,9 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   m->stats.last_fit_kernel_ms = 0.0;
   m->stats.last_fit_launches = 0;
   if (count == 0) return YTM_OK;
-  const Geom& g = m->g;
-  int grid, S, D, cpw;
-  train_shape(m, &grid, &S, &D, &cpw);
+  int cpw;
+  const Geom g = train_geometry(m->g, m->cus, &cpw);  // the training kernels read both
+  const int grid = g.grid, D = g.groups;
   const bool inj = inject != nullptr;
   // One patch and the workgroup's clause state fits in LDS: keep it resident.
   ytm::TrainKind kind = g.P == 1 ? ytm::TrainKind::kGlobalVanilla : ytm::TrainKind::kGlobalConv;
@@ -431,8 +445,6 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.step0 = m->stats.step + (uint64_t)s;
     a.seed = m->params.seed;
     a.N = (int)n;
-    a.S = S;
-    a.D = D;
     a.slot_stride = slot_stride;
     a.cpw = cpw;
     a.rng_slots = rng_slots;

@@ -16,9 +16,9 @@ namespace ytm {
 //   A. each wave takes own clauses: include mask (top plane) vs the sample, all patches
 //      (fast_eval, kernel.cu:255-282), reservoir choice of the firing patch
 //      (select_active, kernel.cu:285-316), patch weight, partial class sums in LDS;
-//   B. the workgroup adds (1<<44 | partial) into its copy of the sample's class-sum
-//      slots (agent-scope atomics; copies keep contention to ~16 workgroups per word),
-//      then waits until every copy holds its full workgroup count;
+//   B. the workgroup adds (1<<44 | partial) into its group's word of the sample's
+//      class-sum row; a two-level tree of agent-scope atomics completes the sum and a
+//      mailbox per group broadcasts it back (exchange_class_sums);
 //   C. clip / target / update probability per class (kernel.cu:397,508-529,543-551);
 //   D. feedback on own clauses (clause_update, kernel.cu:531-613): per class in order,
 //      Q-skip and update draws, Type Ia / Ib / II, weight update, and the literal updates
@@ -200,56 +200,48 @@ struct FbOps {
 
 // Phase D decisions for one non-dropped clause (clause_update, kernel.cu:567-610): per
 // class, the Q-skip and update draws, the feedback type, and the weight update.  The
-// literal updates are left to apply_ops.  Wave-uniform result.
+// literal updates are left to apply_ops.  Wave-uniform result.  Every input is loaded
+// before any decision is taken and the decisions are selects, so the loads overlap
+// instead of forming a chain of dependent LDS round trips.
 template <bool INJECT, bool PRE = false>
 __device__ FbOps decide(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, int sel, int ninc,
                         const int* s_tgt, const double* s_prob, float* wrow, const float* pre_uq,
-                        const float* pre_uu) {
+                        const float* pre_uu, bool dropped = false) {
   const int lane = lane_id();
   const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
   const int kn = g.coalesced ? (int)g.K : 1;
+  const int64_t k = kb + (lane < kn ? lane : 0);  // idle lanes read class kb's inputs and discard them
+  const bool act = lane < kn && !dropped;        // a dropped clause gets no feedback (kernel.cu:555)
+  const int tgt = s_tgt[k];
+  const double prob = s_prob[k];
+  float* wp = wrow + k;
+  const float w0 = *wp;
+  float uq, uu;
+  if (INJECT) {
+    uq = inj[g.C * g.P + c * g.K + k];
+    uu = inj[g.C * g.P + g.C * g.K + c * g.K + k];
+  } else if (PRE) {
+    uq = pre_uq[k];
+    uu = pre_uu[k];
+  } else {
+    const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)k);
+    uq = uniform_from_word(z.x);
+    uu = uniform_from_word(z.y);
+  }
   const bool o = sel >= 0;
   const bool small = o && ninc <= g.maxinc;
-  int type = 0;
-  if (lane < kn) {
-    const int64_t k = kb + lane;
-    const int tgt = s_tgt[k];
-    float uq, uu;
-    if (INJECT) {
-      uq = inj[g.C * g.P + c * g.K + k];
-      uu = inj[g.C * g.P + g.C * g.K + c * g.K + k];
-    } else if (PRE) {
-      uq = pre_uq[k];
-      uu = pre_uu[k];
-    } else {
-      const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)k);
-      uq = uniform_from_word(z.x);
-      uu = uniform_from_word(z.y);
-    }
-    const bool skip = tgt == -1 && (double)uq > g.q_prob;
-    if (!skip) {
-      float* wp = wrow + k;
-      float wv = *wp;
-      const int sign = (wv >= 0.0f) - (wv < 0.0f);
-      const bool upd = (double)uu <= s_prob[k];
-      const int ts = tgt * sign;
-      if (upd) {
-        if (ts > 0 && small) {
-          wv += (float)sign * 1.0f;
-          *wp = wv;
-          type = 1;
-        } else if (ts > 0) {
-          type = 2;
-        } else if (ts < 0 && o) {
-          wv -= (float)sign * 1.0f;
-          if (!g.negative_polarity && wv < 1.0f) wv = 1.0f;
-          *wp = wv;
-          type = 3;
-        }
-      }
-    }
-  }
-  return FbOps{__ballot(type == 1), __ballot(type == 2), __ballot(type == 3)};
+  const bool skip = tgt == -1 && (double)uq > g.q_prob;
+  const int sign = (w0 >= 0.0f) - (w0 < 0.0f);
+  const bool upd = act && !skip && (double)uu <= prob;
+  const int ts = tgt * sign;
+  const bool t1a = upd && ts > 0 && small;
+  const bool t1b = upd && ts > 0 && !small;
+  const bool t2 = upd && ts < 0 && o;
+  const float wa = w0 + (float)sign * 1.0f;
+  float wb = w0 - (float)sign * 1.0f;
+  if (!g.negative_polarity) wb = wb < 1.0f ? 1.0f : wb;
+  if (t1a || t2) *wp = t1a ? wa : wb;
+  return FbOps{__ballot(t1a), __ballot(t1b), __ballot(t2)};
 }
 
 // Literal updates of one clause for the feedback decided in ops, applied class by class
@@ -331,21 +323,22 @@ __device__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, co
                                     long long* s_part, int* s_tgt, double* s_prob, int* s_abort,
                                     uint64_t* wait_ticks) {
   const int lane = lane_id();
-  const int G = gridDim.x, wg = blockIdx.x;
-  const int d = wg / a.S;
-  const unsigned long long gsize = (unsigned long long)min(a.S, G - d * a.S);
+  const int wg = blockIdx.x;
+  const int D = g.groups;
+  const int d = wg / g.group_size;
+  const unsigned long long gsize = (unsigned long long)min(g.group_size, g.grid - d * g.group_size);
   const int ks = ((int)g.K + 15) & ~15;                    // words per row (128-byte multiples)
   unsigned long long* row = a.slots + (int64_t)i * a.slot_stride;
   unsigned long long* group_w = row;                       // [D][ks]
-  unsigned long long* final_w = row + a.D * ks;            // [ks]
+  unsigned long long* final_w = row + D * ks;            // [ks]
   unsigned long long* mbox = final_w + ks;                 // [D][ks]
-  unsigned long long* poll = a.D == 1 ? group_w : mbox + d * ks;
-  const unsigned long long poll_count = a.D == 1 ? gsize : (unsigned long long)a.D;
+  unsigned long long* poll = D == 1 ? group_w : mbox + d * ks;
+  const unsigned long long poll_count = D == 1 ? gsize : (unsigned long long)D;
   if (lane < g.K) {
     const long long part = s_part[lane];
     s_part[lane] = 0;
     const unsigned long long mine = (1ull << 44) + (unsigned long long)part;
-    if (a.D == 1) {
+    if (D == 1) {
       __hip_atomic_fetch_add(&group_w[lane], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
       const unsigned long long now =
@@ -354,8 +347,8 @@ __device__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, co
         const unsigned long long fwd = (1ull << 44) + (now - (gsize << 44));
         const unsigned long long now2 =
             __hip_atomic_fetch_add(&final_w[lane], fwd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + fwd;
-        if (((now2 + (1ull << 43)) >> 44) == (unsigned long long)a.D)
-          for (int m = 0; m < a.D; ++m)
+        if (((now2 + (1ull << 43)) >> 44) == (unsigned long long)D)
+          for (int m = 0; m < D; ++m)
             __hip_atomic_store(&mbox[m * ks + lane], now2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
@@ -590,16 +583,23 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     // ---- A
     for (int idx = wave; idx < n_own; idx += nwv) {
       const int64_t c = c_begin + idx;
+      // Inputs that do not depend on the evaluation are loaded first, so that their LDS
+      // reads overlap those of the include mask and the sample.
+      const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
+      const float wk = s_w[idx * g.K + kp];
+      const bool dropped = s_drop[idx] != 0;
+      const float u1 = INJECT ? -1.0f : s_usel[idx];
       int ninc;
       const int sel = eval_select<true, INJECT, !INJECT>(a, g, inj, c, t, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W,
-                                                         xe, s_drop[idx] != 0, INJECT ? -1.0f : s_usel[idx], &ninc);
+                                                         xe, dropped, u1, &ninc);
       if (lane == 0) {
         s_sel[idx] = sel;
         s_ninc[idx] = ninc;
       }
       if (sel >= 0) {
         if (lane == 0) atomicAdd(&a.patch_w[c], 1);
-        add_partial(a, g, s_part, c, s_w + idx * g.K);
+        if (g.coalesced ? lane < g.K : lane == 0)
+          atomicAdd((unsigned long long*)&s_part[kp], (unsigned long long)(long long)wk);
       }
     }
     YTM_PROF_MARK(0);
@@ -642,10 +642,10 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     }
     // D1: each wave decides its clauses' feedback and queues the ones with updates
     for (int idx = wave; idx < n_own; idx += nwv) {
-      if (s_drop[idx]) continue;
       const int64_t c = c_begin + idx;
       const FbOps ops = decide<INJECT, true>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob, s_w + idx * g.K,
-                                       s_uq + ((i & 1) * a.cpw + idx) * g.K, s_uu + ((i & 1) * a.cpw + idx) * g.K);
+                                             s_uq + ((i & 1) * a.cpw + idx) * g.K, s_uu + ((i & 1) * a.cpw + idx) * g.K,
+                                             s_drop[idx] != 0);
       if ((ops.m1a | ops.m1b | ops.m2) != 0ull && lane == 0) {
         ++my_updates;
         const unsigned long long rng = ops.m1a | ops.m1b;

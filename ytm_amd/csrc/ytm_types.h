@@ -48,7 +48,10 @@ constexpr int kMaxPlanesHost = 16;  // must equal kMaxPlanes of ytm_device.h
   X(double, thresh)        /* T */                                                                   \
   X(double, s_inv)         /* typed S_INV widened to double */                                       \
   X(double, q_prob)        /* typed Q_PROB widened to double */                                      \
-  X(uint32_t, s_thr)       /* floor(s_inv * 2^24) clamped to [0, 2^24] */
+  X(uint32_t, s_thr)       /* floor(s_inv * 2^24) clamped to [0, 2^24] */                             \
+  X(int, grid)             /* training launch: persistent workgroups (0 outside training) */         \
+  X(int, group_size)       /* training launch: workgroups per class-sum group */                     \
+  X(int, groups)           /* training launch: class-sum groups, ceil(grid / group_size) */
 
 struct Geom {
 #define YTM_GEOM_DECL(type, name) type name;
@@ -73,9 +76,7 @@ struct TrainArgs {
   uint64_t step0;
   uint64_t seed;
   int N;
-  int S;                     // workgroups per class-sum group
-  int D;                     // class-sum groups (ceil(grid / S))
-  int64_t slot_stride;       // slot words per sample: D == 1 ? ks : (2D + 1) * ks, ks = K rounded up to 16
+  int64_t slot_stride;       // slot words per sample: groups == 1 ? ks : (2 groups + 1) ks, ks = K rounded to 16
   int cpw;                   // max clauses owned by one workgroup
   int rng_slots;             // literal-draw slots precomputed per sample (resident kernel)
   int profile;               // accumulate per-phase times into counters[4..11]
