@@ -167,8 +167,8 @@ def main() -> int:
             f"({st['last_fit_updates'] / N:.1f}/sample) workgroups {st['train_workgroups']} "
             f"kind {st['train_kind']} wait {st['last_fit_wait_frac']:.3f}")
         if os.environ.get("YTM_TRAIN_PROFILE"):
-            log("[bench]   phase us/sample: A %.2f barA %.2f exch %.2f barBC %.2f D1 %.2f barD1 %.2f D2 %.2f D3 %.2f"
-                % tuple(st["last_fit_phase_us"]))
+            log("[bench]   phase us/sample (wave 0): exchange %.2f barrier %.2f D1 %.2f barrier %.2f D2 %.2f "
+                "D3+re-eval %.2f barrier %.2f" % tuple(st["last_fit_phase_us"][:7]))
 
     # inference over the test set (resident), best of 3 after one warm call
     cs = tm.score_device(dtest)

@@ -357,11 +357,14 @@ int train_rng_slots(int cpw, const Geom& g) {
 
 size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g) {
   if (kind != TrainKind::kResident) return (size_t)2 * cpw * sizeof(int);  // sel, ninc
-  // task masks, planes, weights, 2 samples, sel, ninc, drop, 2 targets, bias, rank-1 draws,
-  // 2x2 class draws, task clause / first slot, slot clause / class, slot plane groups
-  return (size_t)3 * cpw * 8 + (size_t)cpw * (g.np * g.W + g.K) * 4 + (size_t)2 * g.W * 4 + (size_t)3 * cpw * 4 +
-         (size_t)3 * g.K * 4 + (size_t)cpw * 4 + (size_t)4 * cpw * g.K * 4 + (size_t)2 * cpw * 4 +
-         (size_t)2 * rng_slots * 4 + (size_t)rng_slots * g.W * kPreGroups * 4 * 4;
+  // Resident kernel (layout of train_resident_body): task masks [cpw][3] u64; planes
+  // [cpw][np][W]; weights [cpw][K]; samples [3][W]; sel, ninc [2][cpw]; drop, patch
+  // weights [cpw]; targets [3][K]; bias [K]; rank-1 draws [3][cpw]; Q-skip and update
+  // draws [3][cpw][K] each; task clause / first slot [cpw]; slot clause / class [R];
+  // slot plane groups [R][W][kPreGroups][4].
+  const size_t C = (size_t)cpw, K = (size_t)g.K, W = (size_t)g.W, R = (size_t)rng_slots;
+  return 3 * C * 8 + C * (size_t)g.np * W * 4 + C * K * 4 + 3 * W * 4 + 4 * C * 4 + 2 * C * 4 + 3 * K * 4 + K * 4 +
+         3 * C * 4 + 6 * C * K * 4 + 2 * C * 4 + 2 * R * 4 + R * W * kPreGroups * 4 * 4;
 }
 
 static const void* train_fn(TrainKind kind, bool inject) {

@@ -477,19 +477,20 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   }
 }
 
-// Copies sample i (its literal words and its K targets) into LDS buffer i & 1, threads
+// Copies sample i (its literal words and its K targets) into LDS buffer buf, threads
 // [first, first + count) of the workgroup taking part.
-__device__ __forceinline__ void stage_sample(const TrainArgs& a, const Geom& g, int i, uint32_t* s_x, int32_t* s_y, int first,
-                                             int count) {
-  for (int64_t j = first; j < g.W; j += count) s_x[(i & 1) * g.W + j] = a.X[(int64_t)i * g.W + j];
-  for (int64_t j = first; j < g.K; j += count) s_y[(i & 1) * g.K + j] = a.Y[(int64_t)i * g.K + j];
+__device__ __forceinline__ void stage_sample(const TrainArgs& a, const Geom& g, int i, int buf, uint32_t* s_x, int32_t* s_y,
+                                             int first, int count) {
+  for (int64_t j = first; j < g.W; j += count) s_x[buf * g.W + j] = a.X[(int64_t)i * g.W + j];
+  for (int64_t j = first; j < g.K; j += count) s_y[buf * g.K + j] = a.Y[(int64_t)i * g.K + j];
 }
 
-// Counter-stream draws of sample i for the workgroup's clauses, computed ahead of use:
-// the reservoir draw of rank 1 (s_usel[idx]) and the Q-skip / update draws
-// (s_uq / s_uu [i & 1][idx][k]).  Threads [first, first + count) take part.
-__device__ __forceinline__ void precompute_draws(const TrainArgs& a, const Geom& g, int i, int64_t c_begin, int n_own, float* s_usel,
-                                                 float* s_uq, float* s_uu, int first, int count) {
+// Counter-stream draws of sample i for the workgroup's clauses, computed ahead of use
+// into buffer buf: the reservoir draw of rank 1 (s_usel[buf][idx]) and the Q-skip / update
+// draws (s_uq / s_uu [buf][idx][k]).  Threads [first, first + count) take part.
+__device__ __forceinline__ void precompute_draws(const TrainArgs& a, const Geom& g, int i, int buf, int64_t c_begin,
+                                                 int n_own, float* s_usel, float* s_uq, float* s_uu, int first,
+                                                 int count) {
   const uint64_t t = a.step0 + (uint64_t)i;
   const int kn = g.coalesced ? (int)g.K : 1;
   const int per = kn + 1;
@@ -497,53 +498,89 @@ __device__ __forceinline__ void precompute_draws(const TrainArgs& a, const Geom&
     const int idx = j / per, r = j % per;
     const int64_t c = c_begin + idx;
     if (r == kn) {
-      s_usel[idx] = uniform_from_word(site_words(a.seed, t, (uint32_t)c, TAG_SEL, 0u).x);
+      s_usel[buf * a.cpw + idx] = uniform_from_word(site_words(a.seed, t, (uint32_t)c, TAG_SEL, 0u).x);
     } else {
       const int64_t k = (g.coalesced ? 0 : c / g.per_bank) + r;
       const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)k);
-      s_uq[((i & 1) * a.cpw + idx) * g.K + k] = uniform_from_word(z.x);
-      s_uu[((i & 1) * a.cpw + idx) * g.K + k] = uniform_from_word(z.y);
+      s_uq[((int64_t)buf * a.cpw + idx) * g.K + k] = uniform_from_word(z.x);
+      s_uu[((int64_t)buf * a.cpw + idx) * g.K + k] = uniform_from_word(z.y);
     }
   }
 }
 
-// Vanilla TM (one patch) with each workgroup's clause state resident in LDS for the
-// whole launch: planes [own][np][W] and weights [own][K] are loaded once, updated in
-// place and written back at the end.  While wave 0 exchanges the class sums of sample i,
-// the other waves stage sample i+1 (literals and targets) in the second LDS buffer and
-// compute its counter-stream draws.  Each wave owns a fixed subset of the workgroup's
-// clauses for both phases, so two workgroup barriers per sample suffice.
+// Phase A of one resident clause (local index idx) on sample j, by one wave: selection
+// (s_sel), include count (s_ninc), patch weight (s_pw) and the clause's votes added into
+// part.
+template <bool INJECT>
+__device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g, const float* inj, int64_t c_begin, int idx,
+                                              uint64_t t, const uint32_t* s_planes, const float* s_w,
+                                              const int* s_drop, const uint32_t* xe, float u1, int* s_sel,
+                                              int* s_ninc, int* s_pw, long long* part) {
+  const int lane = lane_id();
+  const int64_t c = c_begin + idx;
+  // Inputs that do not depend on the evaluation are loaded first, so that their LDS reads
+  // overlap those of the include mask and the sample.
+  const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
+  const float wk = s_w[idx * g.K + kp];
+  const bool dropped = s_drop[idx] != 0;
+  int ninc;
+  const int sel = eval_select<true, INJECT, !INJECT>(
+      a, g, inj, c, t, s_planes + (int64_t)idx * g.np * g.W + (int64_t)(g.np - 1) * g.W, xe, dropped, u1, &ninc);
+  if (lane == 0) {
+    s_sel[idx] = sel;
+    s_ninc[idx] = ninc;
+    if (sel >= 0) s_pw[idx] += 1;
+  }
+  if (sel >= 0 && (g.coalesced ? lane < g.K : lane == 0))
+    atomicAdd((unsigned long long*)&part[kp], (unsigned long long)(long long)wk);
+}
+
+// Vanilla TM (one patch) with each workgroup's clause state resident in LDS for the whole
+// launch: planes [own][np][W], weights [own][K] and patch weights [own] are loaded once,
+// updated in place and written back at the end.
+//
+// Per sample i, while wave 0 exchanges the class sums of sample i (phases B/C), the other
+// waves evaluate sample i+1 speculatively against the state before i's feedback (phase A
+// of i+1: selections, include counts, patch weights and partial sums), then stage sample
+// i+2 and its counter-stream draws.  Feedback of sample i (phase D) then corrects the
+// speculation exactly: a clause that runs any feedback branch takes back its speculative
+// votes and patch-weight increment (with its weights from before the update), and after
+// its literal updates its owning wave evaluates it again on sample i+1.  Clauses without
+// feedback keep their speculative result, which is exact because their state did not
+// change.  Samples, draws and selections are multi-buffered by sample index.
 template <bool INJECT>
 __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Geom& g) {
   extern __shared__ long long dyn_lds[];
-  __shared__ long long s_part[64];
+  __shared__ long long s_part[2][64];  // partial class sums of samples i and i+1
   __shared__ int s_tgt[64];
   __shared__ double s_prob[64];
   __shared__ int s_abort;
   __shared__ int s_ntask, s_nslot;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-  const int nwv = blockDim.x / kWave;
+  const int nwv = blockDim.x / kWave;  // >= 2 (kTrainThreads)
   const int G = gridDim.x, wg = blockIdx.x;
   const int64_t c_begin = g.C * wg / G, c_end = g.C * (wg + 1) / G;
   const int n_own = (int)(c_end - c_begin);
   const int64_t cw = (int64_t)g.np * g.W;  // plane words per clause
   const int R = a.rng_slots;
+  const int cpw = a.cpw;
   unsigned long long* s_task_m = (unsigned long long*)dyn_lds;    // [cpw][3] feedback masks
-  uint32_t* s_planes = (uint32_t*)(s_task_m + 3 * a.cpw);         // [cpw][np][W]
-  float* s_w = (float*)(s_planes + a.cpw * cw);                   // [cpw][K]
-  uint32_t* s_x = (uint32_t*)(s_w + a.cpw * g.K);                 // [2][W]
-  int* s_sel = (int*)(s_x + 2 * g.W);                             // [cpw]
-  int* s_ninc = s_sel + a.cpw;                                    // [cpw]
-  int* s_drop = s_ninc + a.cpw;                                   // [cpw]
-  int32_t* s_y = s_drop + a.cpw;                                  // [2][K]
-  float* s_bias = (float*)(s_y + 2 * g.K);                        // [K]
-  float* s_usel = s_bias + g.K;                                   // [cpw]
-  float* s_uq = s_usel + a.cpw;                                   // [2][cpw][K]
-  float* s_uu = s_uq + 2 * a.cpw * g.K;                           // [2][cpw][K]
-  int* s_task_idx = (int*)(s_uu + 2 * a.cpw * g.K);               // [cpw]
-  int* s_task_sb = s_task_idx + a.cpw;                            // [cpw] first draw slot
-  int* s_slot_idx = s_task_sb + a.cpw;                            // [R] clause of a draw slot
+  uint32_t* s_planes = (uint32_t*)(s_task_m + 3 * cpw);           // [cpw][np][W]
+  float* s_w = (float*)(s_planes + cpw * cw);                     // [cpw][K]
+  uint32_t* s_x = (uint32_t*)(s_w + cpw * g.K);                   // [3][W]
+  int* s_sel = (int*)(s_x + 3 * g.W);                             // [2][cpw]
+  int* s_ninc = s_sel + 2 * cpw;                                  // [2][cpw]
+  int* s_drop = s_ninc + 2 * cpw;                                 // [cpw]
+  int* s_pw = s_drop + cpw;                                       // [cpw]
+  int32_t* s_y = s_pw + cpw;                                      // [3][K]
+  float* s_bias = (float*)(s_y + 3 * g.K);                        // [K]
+  float* s_usel = s_bias + g.K;                                   // [3][cpw]
+  float* s_uq = s_usel + 3 * cpw;                                 // [3][cpw][K]
+  float* s_uu = s_uq + 3 * cpw * g.K;                             // [3][cpw][K]
+  int* s_task_idx = (int*)(s_uu + 3 * cpw * g.K);                 // [cpw]
+  int* s_task_sb = s_task_idx + cpw;                              // [cpw] first draw slot
+  int* s_slot_idx = s_task_sb + cpw;                              // [R] clause of a draw slot
   int* s_slot_k = s_slot_idx + R;                                 // [R] class of a draw slot
   uint32_t* s_rng = (uint32_t*)(s_slot_k + R);                    // [R][W][kPreGroups][4]
   unsigned long long my_updates = 0ull;
@@ -559,98 +596,87 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     prof_acc[j] += now_ - prof_last;                          \
     prof_last = now_;                                         \
   }
+  auto inj_of = [&](int j) -> const float* { return INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr; };
 
   for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) s_planes[j] = a.planes[c_begin * cw + j];
   for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) s_w[j] = a.weights[c_begin * g.K + j];
-  for (int64_t j = threadIdx.x; j < n_own; j += blockDim.x) s_drop[j] = a.drop[c_begin + j] == 1u;
+  for (int64_t j = threadIdx.x; j < n_own; j += blockDim.x) {
+    s_drop[j] = a.drop[c_begin + j] == 1u;
+    s_pw[j] = a.patch_w[c_begin + j];  // P == 1
+  }
   for (int64_t j = threadIdx.x; j < g.K; j += blockDim.x) s_bias[j] = a.bias[j];
-  stage_sample(a, g, 0, s_x, s_y, threadIdx.x, blockDim.x);
-  if (!INJECT) precompute_draws(a, g, 0, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x, blockDim.x);
-  if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
+  for (int j = 0; j < 2 && j < a.N; ++j) {
+    stage_sample(a, g, j, j, s_x, s_y, threadIdx.x, blockDim.x);
+    if (!INJECT) precompute_draws(a, g, j, j, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x, blockDim.x);
+  }
+  if (threadIdx.x < 128) (&s_part[0][0])[threadIdx.x] = 0;
   if (threadIdx.x == 0) {
     s_abort = 0;
     s_ntask = 0;
     s_nslot = 0;
   }
   __syncthreads();
+  // Phase A of sample 0, every wave.
+  if (a.N > 0)
+    for (int idx = wave; idx < n_own; idx += nwv)
+      resident_eval<INJECT>(a, g, inj_of(0), c_begin, idx, a.step0, s_planes, s_w, s_drop, s_x,
+                            INJECT ? -1.0f : s_usel[idx], s_sel, s_ninc, s_pw, s_part[0]);
+  __syncthreads();
   prof_last = __builtin_amdgcn_s_memrealtime();
 
   for (int i = 0; i < a.N; ++i) {
     const uint64_t t = a.step0 + (uint64_t)i;
-    const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
-    const uint32_t* xe = s_x + (i & 1) * g.W;
-
-    // ---- A
-    for (int idx = wave; idx < n_own; idx += nwv) {
-      const int64_t c = c_begin + idx;
-      // Inputs that do not depend on the evaluation are loaded first, so that their LDS
-      // reads overlap those of the include mask and the sample.
-      const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
-      const float wk = s_w[idx * g.K + kp];
-      const bool dropped = s_drop[idx] != 0;
-      const float u1 = INJECT ? -1.0f : s_usel[idx];
-      int ninc;
-      const int sel = eval_select<true, INJECT, !INJECT>(a, g, inj, c, t, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W,
-                                                         xe, dropped, u1, &ninc);
-      if (lane == 0) {
-        s_sel[idx] = sel;
-        s_ninc[idx] = ninc;
-      }
-      if (sel >= 0) {
-        if (lane == 0) atomicAdd(&a.patch_w[c], 1);
-        if (g.coalesced ? lane < g.K : lane == 0)
-          atomicAdd((unsigned long long*)&s_part[kp], (unsigned long long)(long long)wk);
-      }
-    }
-    YTM_PROF_MARK(0);
-    __syncthreads();
-    YTM_PROF_MARK(1);
-
-    // ---- B + C on wave 0; the other waves stage sample i+1 and its draws
+    const float* inj = inj_of(i);
+    const int b3 = i % 3, b3n = (i + 1) % 3, b2 = i & 1, b2n = b2 ^ 1;
+    const uint32_t* xe = s_x + b3 * g.W;
     const bool more = i + 1 < a.N;
+
+    // ---- B + C on wave 0; speculative A of sample i+1 and staging of i+2 on the others
     if (wave == 0) {
       if (lane == 0) {
         s_ntask = 0;
         s_nslot = 0;
       }
-      exchange_class_sums(a, g, i, s_y + (i & 1) * g.K, s_bias, s_part, s_tgt, s_prob, &s_abort, &wait_ticks);
-      YTM_PROF_MARK(2);
-      if (nwv == 1 && more) {
-        stage_sample(a, g, i + 1, s_x, s_y, lane, kWave);
-        if (!INJECT) precompute_draws(a, g, i + 1, c_begin, n_own, s_usel, s_uq, s_uu, lane, kWave);
+      exchange_class_sums(a, g, i, s_y + b3 * g.K, s_bias, s_part[b2], s_tgt, s_prob, &s_abort, &wait_ticks);
+      YTM_PROF_MARK(0);
+    } else {
+      if (more)
+        for (int idx = wave - 1; idx < n_own; idx += nwv - 1)
+          resident_eval<INJECT>(a, g, inj_of(i + 1), c_begin, idx, t + 1, s_planes, s_w, s_drop, s_x + b3n * g.W,
+                                INJECT ? -1.0f : s_usel[b3n * cpw + idx], s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw,
+                                s_part[b2n]);
+      if (i + 2 < a.N) {
+        const int b3nn = (i + 2) % 3;
+        stage_sample(a, g, i + 2, b3nn, s_x, s_y, threadIdx.x - kWave, blockDim.x - kWave);
+        if (!INJECT)
+          precompute_draws(a, g, i + 2, b3nn, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x - kWave,
+                           blockDim.x - kWave);
       }
-    } else if (more) {
-      stage_sample(a, g, i + 1, s_x, s_y, threadIdx.x - kWave, blockDim.x - kWave);
-      if (!INJECT)
-        precompute_draws(a, g, i + 1, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x - kWave, blockDim.x - kWave);
     }
     __syncthreads();
-    YTM_PROF_MARK(3);
+    YTM_PROF_MARK(1);
     if (s_abort) break;
 
-    // ---- D (no barrier after it: the next phase A of a wave touches only that wave's
-    // own clauses, and every shared buffer it reads was written before a barrier of
-    // this sample)
-    if (INJECT) {
-      for (int idx = wave; idx < n_own; idx += nwv) {
-        if (s_drop[idx]) continue;
-        const bool touched = feedback<INJECT>(a, g, inj, c_begin + idx, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob,
-                                              s_planes + idx * cw, s_w + idx * g.K, xe, nullptr, nullptr);
-        if (touched && lane == 0) ++my_updates;
-      }
-      continue;
-    }
-    // D1: each wave decides its clauses' feedback and queues the ones with updates
+    // ---- D1: each wave decides its own clauses' feedback, takes back the speculative
+    // votes of the clauses that change, and queues them
     for (int idx = wave; idx < n_own; idx += nwv) {
       const int64_t c = c_begin + idx;
-      const FbOps ops = decide<INJECT, true>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob, s_w + idx * g.K,
-                                             s_uq + ((i & 1) * a.cpw + idx) * g.K, s_uu + ((i & 1) * a.cpw + idx) * g.K,
-                                             s_drop[idx] != 0);
-      if ((ops.m1a | ops.m1b | ops.m2) != 0ull && lane == 0) {
+      const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
+      const float wold = s_w[idx * g.K + kp];
+      const FbOps ops = decide<INJECT, !INJECT>(a, g, inj, c, t, s_sel[b2 * cpw + idx], s_ninc[b2 * cpw + idx], s_tgt,
+                                                s_prob, s_w + idx * g.K, s_uq + ((int64_t)b3 * cpw + idx) * g.K,
+                                                s_uu + ((int64_t)b3 * cpw + idx) * g.K, s_drop[idx] != 0);
+      if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
+      if (more && s_sel[b2n * cpw + idx] >= 0) {
+        if (g.coalesced ? lane < g.K : lane == 0)
+          atomicAdd((unsigned long long*)&s_part[b2n][kp], (unsigned long long)(-(long long)wold));
+        if (lane == 0) s_pw[idx] -= 1;
+      }
+      if (lane == 0) {
         ++my_updates;
-        const unsigned long long rng = ops.m1a | ops.m1b;
+        const unsigned long long rng = INJECT ? 0ull : (ops.m1a | ops.m1b);
         const int tk = atomicAdd(&s_ntask, 1);
-        const int sb = atomicAdd(&s_nslot, __popcll(rng));
+        const int sb = INJECT ? 0 : atomicAdd(&s_nslot, __popcll(rng));
         s_task_idx[tk] = idx;
         s_task_sb[tk] = sb;
         s_task_m[tk * 3 + 0] = ops.m1a;
@@ -666,45 +692,55 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         }
       }
     }
-    YTM_PROF_MARK(4);
+    YTM_PROF_MARK(2);
     __syncthreads();
-    YTM_PROF_MARK(5);
+    YTM_PROF_MARK(3);
     const int ntask = s_ntask;
     if (ntask == 0) continue;
-    // D2: the whole workgroup computes the leading plane groups of every queued draw
-    const int nslot = min(s_nslot, R);
-    const int per_slot = (int)g.W * kPreGroups;
-    for (int item = threadIdx.x; item < nslot * per_slot; item += blockDim.x) {
-      const int sl = item / per_slot, rem = item % per_slot;
-      const int64_t w = rem / kPreGroups;
-      const int grp = rem % kPreGroups;
-      const int64_t k = s_slot_k[sl];
-      const U4 z = site_words(a.seed, t, (uint32_t)(c_begin + s_slot_idx[sl]), TAG_LIT,
-                              (uint32_t)((k * g.W + w) * 6 + grp));
-      uint32_t* dst = s_rng + ((int64_t)sl * g.W + w) * (kPreGroups * 4) + grp * 4;
-      dst[0] = z.x;
-      dst[1] = z.y;
-      dst[2] = z.z;
-      dst[3] = z.w;
+    if (!INJECT) {
+      // D2: the whole workgroup computes the leading plane groups of every queued draw
+      const int nslot = min(s_nslot, R);
+      const int per_slot = (int)g.W * kPreGroups;
+      for (int item = threadIdx.x; item < nslot * per_slot; item += blockDim.x) {
+        const int sl = item / per_slot, rem = item % per_slot;
+        const int64_t w = rem / kPreGroups;
+        const int grp = rem % kPreGroups;
+        const int64_t k = s_slot_k[sl];
+        const U4 z = site_words(a.seed, t, (uint32_t)(c_begin + s_slot_idx[sl]), TAG_LIT,
+                                (uint32_t)((k * g.W + w) * 6 + grp));
+        uint32_t* dst = s_rng + ((int64_t)sl * g.W + w) * (kPreGroups * 4) + grp * 4;
+        dst[0] = z.x;
+        dst[1] = z.y;
+        dst[2] = z.z;
+        dst[3] = z.w;
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    YTM_PROF_MARK(6);
-    // D3: the owning wave applies each queued update
+    YTM_PROF_MARK(4);
+    // D3: the owning wave applies each queued update, then evaluates the clause again on
+    // sample i+1 with its new state
     for (int tk = 0; tk < ntask; ++tk) {
       const int idx = s_task_idx[tk];
       if (idx % nwv != wave) continue;
       const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
       const int sb = s_task_sb[tk];
-      const bool have = sb + __popcll(ops.m1a | ops.m1b) <= R;
-      apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[idx], ops, s_planes + idx * cw, xe,
+      const bool have = !INJECT && sb + __popcll(ops.m1a | ops.m1b) <= R;
+      apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[b2 * cpw + idx], ops, s_planes + idx * cw, xe,
                         have ? s_rng + (int64_t)sb * g.W * (kPreGroups * 4) : nullptr);
+      if (more)
+        resident_eval<INJECT>(a, g, inj_of(i + 1), c_begin, idx, t + 1, s_planes, s_w, s_drop, s_x + b3n * g.W,
+                              INJECT ? -1.0f : s_usel[b3n * cpw + idx], s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw,
+                              s_part[b2n]);
     }
-    YTM_PROF_MARK(7);
+    YTM_PROF_MARK(5);
+    __syncthreads();
+    YTM_PROF_MARK(6);
   }
 #undef YTM_PROF_MARK
   __syncthreads();
   for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) a.planes[c_begin * cw + j] = s_planes[j];
   for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) a.weights[c_begin * g.K + j] = s_w[j];
+  for (int64_t j = threadIdx.x; j < n_own; j += blockDim.x) a.patch_w[c_begin + j] = s_pw[j];
   if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
   if (threadIdx.x == 0) {
     atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
@@ -713,6 +749,5 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       for (int j = 0; j < 8; ++j) atomicAdd(&a.counters[4 + j], (unsigned long long)prof_acc[j]);
   }
 }
-
 
 }  // namespace ytm
