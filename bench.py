@@ -167,8 +167,10 @@ def main() -> int:
             f"({st['last_fit_updates'] / N:.1f}/sample) workgroups {st['train_workgroups']} "
             f"kind {st['train_kind']} wait {st['last_fit_wait_frac']:.3f}")
         if os.environ.get("YTM_TRAIN_PROFILE"):
-            log("[bench]   phase us/sample (wave 0): exchange %.2f barrier %.2f D1 %.2f barrier %.2f D2 %.2f "
-                "D3+re-eval %.2f barrier %.2f" % tuple(st["last_fit_phase_us"][:7]))
+            names = (("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier") if st["train_kind"] == 0
+                     else ("A", "barrier", "exchange", "barrier", "D", "barrier"))
+            log("[bench]   phase us/sample (wave 0): "
+                + " ".join(f"{n} {v:.2f}" for n, v in zip(names, st["last_fit_phase_us"])))
 
     # inference over the test set (resident), best of 3 after one warm call
     cs = tm.score_device(dtest)

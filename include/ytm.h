@@ -70,8 +70,11 @@ typedef struct ytm_stats {
     int32_t train_specialised;   /* 1 when the last fit ran a training kernel compiled at run
                                     time for this model's geometry (hipRTC), 0 when it ran the
                                     built-in kernel (YTM_JIT=0, or the compile was unavailable) */
-    double last_fit_phase_us[8]; /* with YTM_TRAIN_PROFILE=1 and the resident kernel:
-                                    average microseconds per sample of each phase */
+    double last_fit_phase_us[8]; /* with YTM_TRAIN_PROFILE=1: average microseconds per sample
+                                    that wave 0 of each workgroup spends in each phase of the
+                                    training kernel (resident: exchange, barrier, D1, barrier,
+                                    D2, D3, barrier; global: A, barrier, exchange, barrier, D,
+                                    barrier) */
 } ytm_stats;
 
 /* Thread-local description of the last failure. */

@@ -399,6 +399,16 @@ __device__ __forceinline__ void add_partial(const TrainArgs& a, const Geom& g, l
   }
 }
 
+// Phase timing of the training kernels: with TrainArgs::profile, wave 0 adds the ticks of
+// the 100 MHz real-time counter since its previous mark to prof_acc[j] (locals `prof`,
+// `prof_acc`, `prof_last` of the kernel body); the host reads the sums from counters[4..11].
+#define YTM_PROF_MARK(j)                                      \
+  if (prof) {                                                 \
+    const uint64_t now_ = __builtin_amdgcn_s_memrealtime();   \
+    prof_acc[j] += now_ - prof_last;                          \
+    prof_last = now_;                                         \
+  }
+
 // Clause state in global memory (L2/MALL resident across samples); any P.
 template <bool VANILLA, bool INJECT>
 __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom& g) {
@@ -418,6 +428,9 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   unsigned long long my_updates = 0ull;
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
+  const bool prof = a.profile && wave == 0;
+  uint64_t prof_acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint64_t prof_last = t_kernel;
   if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_abort = 0;
 
@@ -447,13 +460,17 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         add_partial(a, g, s_part, c, a.weights + c * g.K);
       }
     }
+    YTM_PROF_MARK(0);
     __syncthreads();
+    YTM_PROF_MARK(1);
 
     // ---- B + C
     if (wave == 0)
       exchange_class_sums(a, g, i, a.Y + (int64_t)i * g.K, a.bias, s_part, s_tgt, s_prob, &s_abort, &wait_ticks);
+    YTM_PROF_MARK(2);
     if (threadIdx.x == 0) s_next = 0;
     __syncthreads();
+    YTM_PROF_MARK(3);
     if (s_abort) break;
 
     // ---- D: feedback
@@ -468,12 +485,16 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
                                             a.planes + c * g.np * g.W, a.weights + c * g.K, xe, nullptr, nullptr);
       if (touched && lane == 0) ++my_updates;
     }
+    YTM_PROF_MARK(4);
     __syncthreads();
+    YTM_PROF_MARK(5);
   }
   if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
   if (threadIdx.x == 0) {
     atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
     atomicAdd(&a.counters[2], (unsigned long long)(__builtin_amdgcn_s_memrealtime() - t_kernel));
+    if (prof)
+      for (int j = 0; j < 8; ++j) atomicAdd(&a.counters[4 + j], (unsigned long long)prof_acc[j]);
   }
 }
 
@@ -590,12 +611,6 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   const bool prof = a.profile && wave == 0;
   uint64_t prof_acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   uint64_t prof_last = 0;
-#define YTM_PROF_MARK(j)                                      \
-  if (prof) {                                                 \
-    const uint64_t now_ = __builtin_amdgcn_s_memrealtime();   \
-    prof_acc[j] += now_ - prof_last;                          \
-    prof_last = now_;                                         \
-  }
   auto inj_of = [&](int j) -> const float* { return INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr; };
 
   for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) s_planes[j] = a.planes[c_begin * cw + j];
@@ -736,7 +751,6 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     __syncthreads();
     YTM_PROF_MARK(6);
   }
-#undef YTM_PROF_MARK
   __syncthreads();
   for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) a.planes[c_begin * cw + j] = s_planes[j];
   for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) a.weights[c_begin * g.K + j] = s_w[j];
