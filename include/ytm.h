@@ -92,8 +92,9 @@ int ytm_get_stats(const ytm_model *m, ytm_stats *out);
 int ytm_set_seed(ytm_model *m, uint64_t seed);
 /* Compile (and cache for this process) the training kernel specialised for the geometry
  * of *params and the launch shape used on a device with compute_units CUs (0: 256, an
- * MI355X), without touching a GPU.  train_kind as in ytm_stats (0 resident, 1 global one
- * patch, 2 global several patches); injected != 0 for the injected-draw variant.
+ * MI355X), without touching a GPU.  train_kind as in ytm_stats (0 resident: one patch, or
+ * several with ceil(P/32) <= 64; 1 global one patch; 2 global several patches); injected != 0
+ * for the injected-draw variant.
  * The counterpart of the per-model kernel compile in BaseTM.__init__
  * (src/cutm/base.py:129-159); ytm_fit compiles on first use anyway, so calling this is
  * optional (warm-up, or checking that the compiler is available).  YTM_EHIP with the

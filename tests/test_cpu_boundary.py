@@ -65,7 +65,7 @@ def test_specialised_training_kernels_compile(cfg):
     kw = workloads.make(cfg, 2, 2)[4]
     for injected in (False, True):
         kinds = MultiClassTM.compile_kernels(**kw, injected=injected)
-        assert kinds == ([2] if cfg in (3, 4) else [0, 1])
+        assert kinds == ([0, 2] if cfg in (3, 4) else [0, 1])
 
 
 def test_compile_entry_point_rejects_bad_kind():
@@ -75,7 +75,7 @@ def test_compile_entry_point_rejects_bad_kind():
     tm._skip_gpu_init = True
     tm.__init__(10, 15, 3.9, (12, 1, 1), 2, seed=1)
     params = tm._params()
-    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 2, 0, 0) == 1  # several patches only
+    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 2, 0, 0) == 1  # 2: several patches only
     assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 7, 0, 0) == 1
     assert b"train_kind" in _lib.lib.ytm_last_error()
     assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 0, 0, -1) == 1

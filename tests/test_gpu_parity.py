@@ -83,10 +83,10 @@ def test_fit_counter_stream(cfg, n, clauses, epochs):
         assert_state_equal(tm, ref, f"epoch {epoch}")
 
 
-@pytest.mark.parametrize("cfg,n,clauses", [(1, 3000, None), (2, 200, None), (5, 30, 200)])
+@pytest.mark.parametrize("cfg,n,clauses", [(1, 3000, None), (2, 200, None), (5, 30, 200), (3, 40, 100), (4, 6, 60)])
 def test_fit_global_state_kernel(monkeypatch, cfg, n, clauses):
-    """The one-patch configurations also through the kernel that keeps clause state in
-    global memory (the default keeps it resident in LDS when it fits)."""
+    """Every configuration also through the kernels that keep clause state in global
+    memory (the default keeps it resident in LDS when it fits)."""
     monkeypatch.setenv("YTM_TRAIN_GLOBAL", "1")
     tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses)
     encX = tm.encode(X)
@@ -94,7 +94,7 @@ def test_fit_global_state_kernel(monkeypatch, cfg, n, clauses):
     for epoch in range(2):
         tm.fit(encX, y, is_X_encoded=True)
         upd = ref.fit_encoded(encX, encY)
-        assert tm.stats()["train_kind"] == 1
+        assert tm.stats()["train_kind"] == (1 if tm.number_of_patches == 1 else 2)
         assert tm.stats()["last_fit_updates"] == upd
         assert_state_equal(tm, ref, f"epoch {epoch}")
 
@@ -119,10 +119,8 @@ def test_fit_builtin_kernels(monkeypatch, cfg, n, clauses, global_state, inject)
         upd = ref.fit_encoded(encX, encY, inject=inj)
         st = tm.stats()
         assert st["train_specialised"] == 0
-        if tm.number_of_patches > 1:
-            assert st["train_kind"] == 2
-        elif global_state:
-            assert st["train_kind"] == 1
+        if global_state:
+            assert st["train_kind"] == (2 if tm.number_of_patches > 1 else 1)
         assert st["last_fit_updates"] == upd
         assert_state_equal(tm, ref, f"epoch {epoch}")
 

@@ -192,7 +192,8 @@ class BaseTM:
         tm._skip_gpu_init = True
         tm.__init__(*args, **kwargs)
         params = tm._params()
-        kinds = [0, 1] if tm.number_of_patches == 1 else [2]
+        P = tm.number_of_patches
+        kinds = [0, 1] if P == 1 else ([0, 2] if (P + 31) // 32 <= 64 else [2])
         for kind in kinds:
             check(lib.ytm_compile_train_kernel(ctypes.byref(params), kind, int(bool(injected)), int(compute_units)))
         return kinds

@@ -36,9 +36,10 @@ struct ytm_model {
 
 struct ytm_dataset {
   ytm_model* m;
-  uint32_t* d_X;
-  int32_t* d_Y;
+  uint32_t* d_X;   // [N][P][W]
+  int32_t* d_Y;    // [N][K]
   int64_t N;
+  uint32_t* d_XT;  // [N][L][ceil(P/32)] literal-major copy (several patches), or null
 };
 
 namespace {
@@ -162,6 +163,10 @@ Geom train_geometry(const Geom& model, int cus, int* cpw) {
   int grid, S, D;
   train_shape(model.C, cus, &grid, &S, &D, cpw);
   Geom g = model;
+  // Workgroup size of the specialised kernels (the built-in ones use kTrainThreads).
+  const char* envt = std::getenv("YTM_TRAIN_THREADS");
+  const int t = envt ? std::atoi(envt) : 0;
+  g.threads = (t >= 128 && t <= 1024 && t % 64 == 0) ? t : ytm::kTrainThreads;
   g.grid = grid;
   g.group_size = S;
   g.groups = D;
@@ -244,8 +249,9 @@ int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injec
   if (rc) return rc;
   int cpw;
   const Geom g = train_geometry(model, compute_units > 0 ? compute_units : 256, &cpw);
-  if ((g.P == 1) != (train_kind != 2))
-    return fail(YTM_EINVAL, "train_kind 2 is for several patches, 0 and 1 for one patch");
+  const bool valid = train_kind == 1 ? g.P == 1 : train_kind == 2 ? g.P > 1 : (g.P == 1 || ytm::literal_major(g));
+  if (!valid)
+    return fail(YTM_EINVAL, "train_kind 1 is for one patch, 2 for several, 0 for one patch or a literal-major model");
   std::vector<char> code;
   std::string why;
   if (!ytm::jit_compile(g, (ytm::TrainKind)train_kind, injected != 0, &code, &why))
@@ -315,9 +321,16 @@ int ytm_dataset_create(ytm_model* m, const uint32_t* encX, const int32_t* encY, 
   if (!m || !out || N < 0 || (N > 0 && !encX)) return fail(YTM_EINVAL, "bad dataset arguments");
   *out = nullptr;
   const Geom& g = m->g;
-  ytm_dataset* ds = new ytm_dataset{m, nullptr, nullptr, N};
+  ytm_dataset* ds = new ytm_dataset{m, nullptr, nullptr, N, nullptr};
   int rc = upload((void**)&ds->d_X, encX, (size_t)(N * g.P * g.W) * 4, m->stream);
   if (!rc && encY) rc = upload((void**)&ds->d_Y, encY, (size_t)(N * g.K) * 4, m->stream);
+  if (!rc && ytm::literal_major(g) && N > 0) {
+    // Several patches: the training kernel evaluates clauses on a literal-major copy.
+    const size_t bytes = (size_t)(N * g.L * ((g.P + 31) / 32)) * 4;
+    hipError_t e = hipMalloc(&ds->d_XT, bytes);
+    if (e == hipSuccess) e = ytm::launch_transpose(ds->d_X, N, ds->d_XT, g, m->stream);
+    if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("literal-major copy: ") + hipGetErrorString(e));
+  }
   if (!rc) {
     hipError_t e = hipStreamSynchronize(m->stream);
     if (e != hipSuccess) rc = fail(YTM_EHIP, hipGetErrorString(e));
@@ -334,6 +347,7 @@ void ytm_dataset_destroy(ytm_dataset* ds) {
   if (!ds) return;
   if (ds->d_X) (void)hipFree(ds->d_X);
   if (ds->d_Y) (void)hipFree(ds->d_Y);
+  if (ds->d_XT) (void)hipFree(ds->d_XT);
   delete ds;
 }
 
@@ -348,13 +362,14 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   m->stats.last_fit_launches = 0;
   if (count == 0) return YTM_OK;
   int cpw;
-  const Geom g = train_geometry(m->g, m->cus, &cpw);  // the training kernels read both
+  Geom g = train_geometry(m->g, m->cus, &cpw);  // the training kernels read both
   const int grid = g.grid, D = g.groups;
   const bool inj = inject != nullptr;
-  // One patch and the workgroup's clause state fits in LDS: keep it resident.
+  // Keep the workgroup's clause state resident in LDS when it fits (with several patches,
+  // together with two literal-major samples).
   ytm::TrainKind kind = g.P == 1 ? ytm::TrainKind::kGlobalVanilla : ytm::TrainKind::kGlobalConv;
   const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
-  if (g.P == 1 && !(force_global && std::atoi(force_global) > 0) &&
+  if ((g.P == 1 || ytm::literal_major(g)) && !(force_global && std::atoi(force_global) > 0) &&
       ytm::train_lds_bytes(ytm::TrainKind::kResident, cpw, ytm::train_rng_slots(cpw, g), g) <= kResidentLdsLimit)
     kind = ytm::TrainKind::kResident;
   const int rng_slots = kind == ytm::TrainKind::kResident ? ytm::train_rng_slots(cpw, g) : 0;
@@ -369,9 +384,10 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     if (!jit_fn && jit_env && std::atoi(jit_env) == 2)
       return fail(YTM_EHIP, "specialised training kernel unavailable: " + why);
   }
+  if (!jit_fn) g.threads = ytm::kTrainThreads;
   int bpc = 0;
   if (jit_fn)
-    HIP_TRY(ytm::jit_occupancy(jit_fn, lds, &bpc));
+    HIP_TRY(ytm::jit_occupancy(jit_fn, g.threads, lds, &bpc));
   else
     HIP_TRY(ytm::train_occupancy(kind, inj, lds, &bpc));
   if ((int64_t)bpc * m->cus < grid)
@@ -434,6 +450,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.patch_w = m->d_pw;
     a.bias = m->d_bias;
     a.X = ds->d_X + (first + s) * g.P * g.W;
+    a.XT = ds->d_XT ? ds->d_XT + (first + s) * g.L * ((g.P + 31) / 32) : nullptr;
     a.Y = ds->d_Y + (first + s) * g.K;
     a.drop = d_drop;
     a.inject = d_inj;
@@ -453,7 +470,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.g = g;
     FIT_TRY(hipEventRecord(m->ev0, m->stream));
     if (jit_fn)
-      FIT_TRY(ytm::launch_train_jit(jit_fn, a, grid, lds, m->stream));
+      FIT_TRY(ytm::launch_train_jit(jit_fn, a, grid, g.threads, lds, m->stream));
     else
       FIT_TRY(ytm::launch_train(a, grid, lds, kind, inj, m->stream));
     FIT_TRY(hipEventRecord(m->ev1, m->stream));

@@ -11,6 +11,8 @@
 namespace ytm {
 
 hipError_t launch_encode(const uint32_t* X, int64_t N, uint32_t* out, const Geom& g, hipStream_t s);
+// Literal-major copy of encoded samples (several patches): XT [N][L][ceil(P/32)].
+hipError_t launch_transpose(const uint32_t* X, int64_t N, uint32_t* XT, const Geom& g, hipStream_t s);
 hipError_t launch_ta_to_planes(const uint32_t* ta, uint32_t* planes, const Geom& g, hipStream_t s);
 hipError_t launch_planes_to_ta(const uint32_t* planes, uint32_t* ta, const Geom& g, hipStream_t s);
 hipError_t launch_init_state(uint32_t* planes, float* w, const Geom& g, uint64_t seed, hipStream_t s);
@@ -39,7 +41,8 @@ int train_rng_slots(int cpw, const Geom& g);
 bool jit_enabled();
 bool jit_compile(const Geom& g, TrainKind kind, bool inject, std::vector<char>* code, std::string* why);
 hipFunction_t jit_train_kernel(const Geom& g, TrainKind kind, bool inject, std::string* why);
-hipError_t jit_occupancy(hipFunction_t fn, size_t lds_bytes, int* blocks_per_cu);
-hipError_t launch_train_jit(hipFunction_t fn, const TrainArgs& a, int grid, size_t lds_bytes, hipStream_t s);
+hipError_t jit_occupancy(hipFunction_t fn, int threads, size_t lds_bytes, int* blocks_per_cu);
+hipError_t launch_train_jit(hipFunction_t fn, const TrainArgs& a, int grid, int threads, size_t lds_bytes,
+                            hipStream_t s);
 
 }  // namespace ytm

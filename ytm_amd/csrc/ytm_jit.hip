@@ -54,7 +54,7 @@ std::string kernel_source(const Geom& g, TrainKind kind, bool inject) {
 #undef YTM_GEOM_PRINT
   s += "};\n}  // namespace ytm\n";
   const char* inj = inject ? "true" : "false";
-  s += "extern \"C\" __global__ __launch_bounds__(ytm::kTrainThreads) void ";
+  s += "extern \"C\" __global__ __launch_bounds__(" + std::to_string(g.threads) + ") void ";
   s += kernel_name(kind);
   s += "(ytm::TrainArgs a) {\n  ";
   switch (kind) {
@@ -183,14 +183,15 @@ hipFunction_t jit_train_kernel(const Geom& g, TrainKind kind, bool inject, std::
   return fn;
 }
 
-hipError_t jit_occupancy(hipFunction_t fn, size_t lds_bytes, int* blocks_per_cu) {
-  return hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kTrainThreads, lds_bytes);
+hipError_t jit_occupancy(hipFunction_t fn, int threads, size_t lds_bytes, int* blocks_per_cu) {
+  return hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, threads, lds_bytes);
 }
 
-hipError_t launch_train_jit(hipFunction_t fn, const TrainArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+hipError_t launch_train_jit(hipFunction_t fn, const TrainArgs& a, int grid, int threads, size_t lds_bytes,
+                            hipStream_t s) {
   TrainArgs copy = a;
   void* args[] = {&copy};
-  return hipModuleLaunchCooperativeKernel(fn, (unsigned)grid, 1, 1, kTrainThreads, 1, 1, (unsigned)lds_bytes, s,
+  return hipModuleLaunchCooperativeKernel(fn, (unsigned)grid, 1, 1, (unsigned)threads, 1, 1, (unsigned)lds_bytes, s,
                                           args);
 }
 

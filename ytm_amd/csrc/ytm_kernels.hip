@@ -66,6 +66,38 @@ __global__ __launch_bounds__(256) void encode_kernel(const uint32_t* __restrict_
   }
 }
 
+// Literal-major copy of encoded samples with several patches: bit b of XT[e][l][j] is
+// literal l of patch 32j + b (0 beyond P), PW = ceil(P / 32) words per literal.  One wave
+// per (sample, literal word w, chunk of 64 patches): lane q holds word w of patch
+// 64*chunk + q, and one ballot per bit gives a literal's 64-patch bitset.
+__global__ __launch_bounds__(256) void transpose_kernel(const uint32_t* __restrict__ X, int64_t N, Geom g,
+                                                        uint32_t* __restrict__ XT) {
+  const int lane = lane_id();
+  const int64_t PW = (g.P + 31) / 32;
+  const int64_t nchunk = (g.P + kWave - 1) / kWave;
+  const int64_t items = N * g.W * nchunk;
+  const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / kWave;
+  const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
+  for (int64_t item = wave; item < items; item += nwaves) {
+    const int64_t e = item / (g.W * nchunk), rem = item % (g.W * nchunk);
+    const int64_t w = rem / nchunk, ch = rem % nchunk;
+    const int64_t p = ch * kWave + lane;
+    const uint32_t xw = p < g.P ? X[(e * g.P + p) * g.W + w] : 0u;
+    unsigned long long keep = 0ull;
+#pragma unroll
+    for (int b = 0; b < 32; ++b) {
+      const unsigned long long bits = __ballot((xw >> b) & 1u);
+      if (lane == b) keep = bits;
+    }
+    const int64_t l = 32 * w + lane;
+    if (lane < 32 && l < g.L) {
+      uint32_t* dst = XT + (e * g.L + l) * PW + 2 * ch;
+      dst[0] = (uint32_t)keep;
+      if (2 * ch + 1 < PW) dst[1] = (uint32_t)(keep >> 32);
+    }
+  }
+}
+
 // ===================================================================== TA state I/O
 // uint32 (C, L) states <-> bit-planes.  Literals >= L of the last word hold s = 0 and are
 // never updated or included.
@@ -289,6 +321,12 @@ hipError_t launch_encode(const uint32_t* X, int64_t N, uint32_t* out, const Geom
   return hipGetLastError();
 }
 
+hipError_t launch_transpose(const uint32_t* X, int64_t N, uint32_t* XT, const Geom& g, hipStream_t s) {
+  const int64_t waves = N * g.W * ((g.P + kWave - 1) / kWave);
+  transpose_kernel<<<grid_for(waves * kWave, 256), 256, 0, s>>>(X, N, g, XT);
+  return hipGetLastError();
+}
+
 hipError_t launch_ta_to_planes(const uint32_t* ta, uint32_t* planes, const Geom& g, hipStream_t s) {
   ta_to_planes_kernel<<<grid_for(g.C * g.W, 256), 256, 0, s>>>(ta, planes, g);
   return hipGetLastError();
@@ -356,15 +394,18 @@ int train_rng_slots(int cpw, const Geom& g) {
 }
 
 size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g) {
-  if (kind != TrainKind::kResident) return (size_t)2 * cpw * sizeof(int);  // sel, ninc
+  if (kind != TrainKind::kResident)  // sel, ninc [cpw]; the literal-major sample [L][PW]
+    return (size_t)2 * cpw * sizeof(int) + (literal_major_lds(g) ? (size_t)(g.L * ((g.P + 31) / 32)) * 4 : 0);
   // Resident kernel (layout of train_resident_body): task masks [cpw][3] u64; planes
   // [cpw][np][W]; weights [cpw][K]; samples [3][W]; sel, ninc [2][cpw]; drop, patch
   // weights [cpw]; targets [3][K]; bias [K]; rank-1 draws [3][cpw]; Q-skip and update
   // draws [3][cpw][K] each; task clause / first slot [cpw]; slot clause / class [R];
   // slot plane groups [R][W][kPreGroups][4].
+  // Several patches add the literal-major samples [2][L][PW] after the task masks.
   const size_t C = (size_t)cpw, K = (size_t)g.K, W = (size_t)g.W, R = (size_t)rng_slots;
-  return 3 * C * 8 + C * (size_t)g.np * W * 4 + C * K * 4 + 3 * W * 4 + 4 * C * 4 + 2 * C * 4 + 3 * K * 4 + K * 4 +
-         3 * C * 4 + 6 * C * K * 4 + 2 * C * 4 + 2 * R * 4 + R * W * kPreGroups * 4 * 4;
+  const size_t xt = g.P > 1 ? (size_t)(2 * g.L * ((g.P + 31) / 32)) * 4 : 0;
+  return 3 * C * 8 + xt + C * (size_t)g.np * W * 4 + C * K * 4 + 3 * W * 4 + 4 * C * 4 + 2 * C * 4 + 3 * K * 4 +
+         K * 4 + 3 * C * 4 + 6 * C * K * 4 + 2 * C * 4 + 2 * R * 4 + R * W * kPreGroups * 4 * 4;
 }
 
 static const void* train_fn(TrainKind kind, bool inject) {

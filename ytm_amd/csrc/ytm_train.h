@@ -89,6 +89,132 @@ __device__ __forceinline__ uint32_t literal_draw_mask(const TrainArgs& a, const 
   }
 }
 
+// Reservoir choice among R >= 1 firing patches (select_active, kernel.cu:285-316): the rank
+// r (1-based, in patch order) of the selected patch is the highest r whose draw is below
+// 1.0f / r, or 0 when none is.  Ranks are scanned from R downward, 256 (64 Philox calls) at
+// a time.  Wave-uniform.
+template <bool INJECT>
+__device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t,
+                                              int R) {
+  const int lane = lane_id();
+  int best = 0;
+  for (int g0 = (R - 1) >> 2; g0 >= 0; g0 -= kWave) {
+    const int gl = g0 - lane;
+    int lb = 0;
+    if (gl >= 0) {
+      if (INJECT) {
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * gl + 1 + j;
+          if (r <= R && inj[c * g.P + (r - 1)] < a.inv_rank[r]) lb = r;
+        }
+      } else {
+        const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * gl + 1 + j;
+          if (r <= R && uniform_from_word(word_of(z, j)) < a.inv_rank[r]) lb = r;
+        }
+      }
+    }
+    best = wave_max_i32(lb);
+    if (best > 0) break;
+  }
+  return best;
+}
+
+// Phase A for one clause of a model with several patches, on the literal-major sample xt
+// ([L][PW] words, PW = ceil(P/32) <= 64; bit b of word j of literal l: literal l set in
+// patch 32j + b).  The clause fires on the patches where every included literal is set,
+// so its firing bitmap is the AND of its included literals' bitsets (fast_eval,
+// kernel.cu:255-282): lane j keeps patch word j, the included literals are walked 8 at a
+// time (a short batch repeats its last literal, AND being idempotent) and the walk stops
+// once no patch can fire.  Then the reservoir choice as in eval_select.  Wave-uniform.
+template <bool INJECT>
+__device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, const uint32_t* m,
+                              const uint32_t* xt, bool dropped, int* ninc_out) {
+  const int lane = lane_id();
+  const bool exact_count = g.maxinc < g.L;
+  const int PW = (int)((g.P + 31) / 32);
+  int cnt = 0;
+  uint32_t any = 0u;
+  for (int64_t w = lane; w < g.W; w += kWave) {
+    const uint32_t mw = m[w];
+    if (exact_count) cnt += __popc(mw);
+    any |= mw;
+  }
+  const int ninc = exact_count ? wave_sum_i32(cnt) : (__any(any != 0u) ? 1 : 0);
+  *ninc_out = ninc;
+  if (dropped) return -1;
+  uint32_t acc = 0u;
+  if (lane < PW) acc = (lane == PW - 1 && (g.P & 31)) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu;
+  if (ninc != 0) {  // an empty clause fires on every patch in training
+    const int jl = lane < PW ? lane : 0;
+    bool alive = true;
+    for (int64_t wb = 0; wb < g.W && alive; wb += kWave) {
+      // lane q holds mask word wb + q; lane j of each round of 64 finds the j-th included
+      // literal of the chunk (binary search over the prefix counts, then a select)
+      const uint32_t mv = wb + lane < g.W ? m[wb + lane] : 0u;
+      const int pc = __popc(mv);
+      const int incl = wave_inclusive_scan(pc);
+      const int tot = __shfl(incl, kWave - 1);
+      for (int jb = 0; jb < tot && alive; jb += kWave) {
+        const int j = jb + lane;
+        int q = 0;  // first lane whose inclusive count exceeds j
+#pragma unroll
+        for (int step = kWave / 2; step > 0; step >>= 1)
+          if (__shfl(incl, q + step - 1) <= j) q += step;
+        const uint32_t mw = __shfl(mv, q);
+        int r = j - (__shfl(incl, q) - __shfl(pc, q));  // rank of the literal within word q
+        uint32_t v = mw;
+        int pos = 0;
+#pragma unroll
+        for (int width = 16; width > 0; width >>= 1) {
+          const int lowc = __popc(v & ((1u << width) - 1u));
+          if (r >= lowc) {
+            r -= lowc;
+            v >>= width;
+            pos += width;
+          }
+        }
+        const int lit = (int)(32 * (wb + q)) + pos;  // valid for lanes j < tot
+        const int cnt = tot - jb < kWave ? tot - jb : kWave;
+        for (int jj = 0; jj < cnt; jj += 8) {
+          uint32_t vv = 0xFFFFFFFFu;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            // a short last batch repeats literal jj (AND is idempotent)
+            const int l = __builtin_amdgcn_readlane(lit, jj + u < cnt ? jj + u : jj);
+            vv &= xt[l * PW + jl];
+          }
+          acc &= vv;
+          if (((jj >> 3) & 1) && !__any(acc != 0u)) {  // every 16 literals: stop once nothing fires
+            alive = false;
+            break;
+          }
+        }
+      }
+    }
+  }
+  const int pc = lane < PW ? __popc(acc) : 0;
+  const int incl = wave_inclusive_scan(pc);
+  const int R = __shfl(incl, kWave - 1);
+  if (R == 0) return -1;
+  const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R);
+  if (best == 0) return -1;
+  // Patch of the best-th set bit of the firing bitmap.
+  const int excl = incl - pc;
+  const bool here = lane < PW && best > excl && best <= incl;
+  const unsigned long long hb = __ballot(here);
+  const int src = __ffsll((long long)hb) - 1;
+  int pos = 0;
+  if (lane == src) {
+    uint32_t v = acc;
+    for (int q = 1; q < best - excl; ++q) v &= v - 1u;
+    pos = src * 32 + __builtin_ctz(v);
+  }
+  return __shfl(pos, src);
+}
+
 // Phase A for one clause (wave-uniform): returns the selected patch or -1 and the
 // clause's include count.  m: the clause's include mask (W words), xe: the sample (P*W).
 template <bool VANILLA, bool INJECT, bool PRE = false>
@@ -152,30 +278,7 @@ __device__ int eval_select(const TrainArgs& a, const Geom& g, const float* inj, 
       R += __popcll(b);
     }
     if (R == 0) return -1;
-    // Reservoir: the selected firing patch is the one of highest rank r whose draw is
-    // below 1.0f / r; scan ranks from R downward, 256 ranks (64 Philox calls) at a time.
-    int best = 0;
-    for (int g0 = (R - 1) >> 2; g0 >= 0; g0 -= kWave) {
-      const int gl = g0 - lane;
-      int lb = 0;
-      if (gl >= 0) {
-        if (INJECT) {
-          for (int j = 0; j < 4; ++j) {
-            const int r = 4 * gl + 1 + j;
-            if (r <= R && inj[c * g.P + (r - 1)] < a.inv_rank[r]) lb = r;
-          }
-        } else {
-          const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int r = 4 * gl + 1 + j;
-            if (r <= R && uniform_from_word(word_of(z, j)) < a.inv_rank[r]) lb = r;
-          }
-        }
-      }
-      best = wave_max_i32(lb);
-      if (best > 0) break;
-    }
+    const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R);
     if (best == 0) return -1;
     // Patch of the best-th set bit of the firing bitmap.
     const int pc = lane < nch ? __popcll(myfire) : 0;
@@ -425,6 +528,8 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   const int n_own = (int)(c_end - c_begin);
   int* s_sel = (int*)dyn_lds;                          // [cpw]
   int* s_ninc = s_sel + a.cpw;                         // [cpw]
+  uint32_t* s_xt = (uint32_t*)(s_ninc + a.cpw);        // [L][PW] when literal_major_lds(g)
+  const int64_t xt_words = literal_major(g) ? g.L * ((g.P + 31) / 32) : 0;
   unsigned long long my_updates = 0ull;
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
@@ -438,6 +543,20 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     const uint64_t t = a.step0 + (uint64_t)i;
     const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
     const uint32_t* xe = a.X + (int64_t)i * g.P * g.W;
+    const uint32_t* xt = nullptr;  // literal-major sample
+    if (!VANILLA && literal_major(g)) {
+      xt = a.XT + (int64_t)i * xt_words;
+      if (literal_major_lds(g)) {
+        if ((xt_words & 1) == 0) {  // 8-byte copies: s_xt and every sample start are 8-byte aligned
+          const uint2* src = (const uint2*)xt;
+          uint2* dst = (uint2*)s_xt;
+          for (int64_t j = threadIdx.x; j < xt_words / 2; j += blockDim.x) dst[j] = src[j];
+        } else {
+          for (int64_t j = threadIdx.x; j < xt_words; j += blockDim.x) s_xt[j] = xt[j];
+        }
+        xt = s_xt;
+      }
+    }
     if (threadIdx.x == 0) s_next = 0;
     __syncthreads();
 
@@ -449,8 +568,10 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       if (idx >= n_own) break;
       const int64_t c = c_begin + idx;
       int ninc;
-      const int sel = eval_select<VANILLA, INJECT>(a, g, inj, c, t, a.planes + (c * g.np + g.np - 1) * g.W, xe,
-                                                   a.drop[c] == 1u, -1.0f, &ninc);
+      const uint32_t* m = a.planes + (c * g.np + g.np - 1) * g.W;
+      const int sel = (!VANILLA && literal_major(g))
+                          ? eval_select_lm<INJECT>(a, g, inj, c, t, m, xt, a.drop[c] == 1u, &ninc)
+                          : eval_select<VANILLA, INJECT>(a, g, inj, c, t, m, xe, a.drop[c] == 1u, -1.0f, &ninc);
       if (lane == 0) {
         s_sel[idx] = sel;
         s_ninc[idx] = ninc;
@@ -498,11 +619,12 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   }
 }
 
-// Copies sample i (its literal words and its K targets) into LDS buffer buf, threads
-// [first, first + count) of the workgroup taking part.
+// Copies sample i (with one patch, its literal words; its K targets) into LDS buffer buf,
+// threads [first, first + count) of the workgroup taking part.
 __device__ __forceinline__ void stage_sample(const TrainArgs& a, const Geom& g, int i, int buf, uint32_t* s_x, int32_t* s_y,
                                              int first, int count) {
-  for (int64_t j = first; j < g.W; j += count) s_x[buf * g.W + j] = a.X[(int64_t)i * g.W + j];
+  if (g.P == 1)  // several patches: the clauses read the literal-major sample instead
+    for (int64_t j = first; j < g.W; j += count) s_x[buf * g.W + j] = a.X[(int64_t)i * g.W + j];
   for (int64_t j = first; j < g.K; j += count) s_y[buf * g.K + j] = a.Y[(int64_t)i * g.K + j];
 }
 
@@ -529,36 +651,65 @@ __device__ __forceinline__ void precompute_draws(const TrainArgs& a, const Geom&
   }
 }
 
+// Copies the literal-major sample i ([L][PW] words) into LDS buffer buf of s_xt, threads
+// [first, first + count) taking part (8-byte copies when the word count is even: s_xt and
+// every sample start are then 8-byte aligned).
+__device__ __forceinline__ void stage_xt(const TrainArgs& a, const Geom& g, int i, int buf, uint32_t* s_xt, int first,
+                                         int count) {
+  const int64_t n = g.L * ((g.P + 31) / 32);
+  const uint32_t* src = a.XT + (int64_t)i * n;
+  uint32_t* dst = s_xt + (int64_t)buf * n;
+  if ((n & 1) == 0) {
+    for (int64_t j = first; j < n / 2; j += count) ((uint2*)dst)[j] = ((const uint2*)src)[j];
+  } else {
+    for (int64_t j = first; j < n; j += count) dst[j] = src[j];
+  }
+}
+
 // Phase A of one resident clause (local index idx) on sample j, by one wave: selection
-// (s_sel), include count (s_ninc), patch weight (s_pw) and the clause's votes added into
-// part.
+// (sel[idx]), include count (ninc[idx]), patch weight and the clause's votes added into
+// part.  One patch: the sample's words are s_x[j % 3], the rank-1 draw s_usel[j % 3] and
+// the patch weight s_pw[idx]; several patches: the literal-major sample is s_xt[j & 1] and
+// the patch weight is counted in global memory.
 template <bool INJECT>
-__device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g, const float* inj, int64_t c_begin, int idx,
-                                              uint64_t t, const uint32_t* s_planes, const float* s_w,
-                                              const int* s_drop, const uint32_t* xe, float u1, int* s_sel,
-                                              int* s_ninc, int* s_pw, long long* part) {
+__device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int idx,
+                                              const uint32_t* s_planes, const float* s_w, const int* s_drop,
+                                              const uint32_t* s_x, const uint32_t* s_xt, const float* s_usel,
+                                              int* sel_out, int* ninc_out, int* s_pw, long long* part) {
   const int lane = lane_id();
   const int64_t c = c_begin + idx;
+  const uint64_t t = a.step0 + (uint64_t)j;
+  const float* inj = INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr;
   // Inputs that do not depend on the evaluation are loaded first, so that their LDS reads
   // overlap those of the include mask and the sample.
   const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
   const float wk = s_w[idx * g.K + kp];
   const bool dropped = s_drop[idx] != 0;
-  int ninc;
-  const int sel = eval_select<true, INJECT, !INJECT>(
-      a, g, inj, c, t, s_planes + (int64_t)idx * g.np * g.W + (int64_t)(g.np - 1) * g.W, xe, dropped, u1, &ninc);
+  const uint32_t* m = s_planes + (int64_t)idx * g.np * g.W + (int64_t)(g.np - 1) * g.W;
+  int ninc, sel;
+  if (g.P == 1)
+    sel = eval_select<true, INJECT, !INJECT>(a, g, inj, c, t, m, s_x + (j % 3) * g.W, dropped,
+                                             INJECT ? -1.0f : s_usel[(j % 3) * a.cpw + idx], &ninc);
+  else
+    sel = eval_select_lm<INJECT>(a, g, inj, c, t, m, s_xt + (int64_t)(j & 1) * g.L * ((g.P + 31) / 32), dropped, &ninc);
   if (lane == 0) {
-    s_sel[idx] = sel;
-    s_ninc[idx] = ninc;
-    if (sel >= 0) s_pw[idx] += 1;
+    sel_out[idx] = sel;
+    ninc_out[idx] = ninc;
+    if (sel >= 0) {
+      if (g.P == 1)
+        s_pw[idx] += 1;
+      else
+        atomicAdd(&a.patch_w[c * g.P + sel], 1);
+    }
   }
   if (sel >= 0 && (g.coalesced ? lane < g.K : lane == 0))
     atomicAdd((unsigned long long*)&part[kp], (unsigned long long)(long long)wk);
 }
 
-// Vanilla TM (one patch) with each workgroup's clause state resident in LDS for the whole
-// launch: planes [own][np][W], weights [own][K] and patch weights [own] are loaded once,
-// updated in place and written back at the end.
+// Training with each workgroup's clause state resident in LDS for the whole launch:
+// planes [own][np][W], weights [own][K] (and, with one patch, patch weights [own]) are
+// loaded once, updated in place and written back at the end.  With several patches the
+// clauses are evaluated on the literal-major samples, double-buffered in LDS.
 //
 // Per sample i, while wave 0 exchanges the class sums of sample i (phases B/C), the other
 // waves evaluate sample i+1 speculatively against the state before i's feedback (phase A
@@ -586,8 +737,10 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   const int64_t cw = (int64_t)g.np * g.W;  // plane words per clause
   const int R = a.rng_slots;
   const int cpw = a.cpw;
+  const int64_t xtw = g.P > 1 ? g.L * ((g.P + 31) / 32) : 0;     // literal-major sample words
   unsigned long long* s_task_m = (unsigned long long*)dyn_lds;    // [cpw][3] feedback masks
-  uint32_t* s_planes = (uint32_t*)(s_task_m + 3 * cpw);           // [cpw][np][W]
+  uint32_t* s_xt = (uint32_t*)(s_task_m + 3 * cpw);               // [2][L][PW] (several patches)
+  uint32_t* s_planes = s_xt + 2 * xtw;                            // [cpw][np][W]
   float* s_w = (float*)(s_planes + cpw * cw);                     // [cpw][K]
   uint32_t* s_x = (uint32_t*)(s_w + cpw * g.K);                   // [3][W]
   int* s_sel = (int*)(s_x + 3 * g.W);                             // [2][cpw]
@@ -611,17 +764,17 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   const bool prof = a.profile && wave == 0;
   uint64_t prof_acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   uint64_t prof_last = 0;
-  auto inj_of = [&](int j) -> const float* { return INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr; };
 
   for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) s_planes[j] = a.planes[c_begin * cw + j];
   for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) s_w[j] = a.weights[c_begin * g.K + j];
   for (int64_t j = threadIdx.x; j < n_own; j += blockDim.x) {
     s_drop[j] = a.drop[c_begin + j] == 1u;
-    s_pw[j] = a.patch_w[c_begin + j];  // P == 1
+    if (g.P == 1) s_pw[j] = a.patch_w[c_begin + j];
   }
   for (int64_t j = threadIdx.x; j < g.K; j += blockDim.x) s_bias[j] = a.bias[j];
   for (int j = 0; j < 2 && j < a.N; ++j) {
     stage_sample(a, g, j, j, s_x, s_y, threadIdx.x, blockDim.x);
+    if (g.P > 1) stage_xt(a, g, j, j, s_xt, threadIdx.x, blockDim.x);
     if (!INJECT) precompute_draws(a, g, j, j, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x, blockDim.x);
   }
   if (threadIdx.x < 128) (&s_part[0][0])[threadIdx.x] = 0;
@@ -634,16 +787,17 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   // Phase A of sample 0, every wave.
   if (a.N > 0)
     for (int idx = wave; idx < n_own; idx += nwv)
-      resident_eval<INJECT>(a, g, inj_of(0), c_begin, idx, a.step0, s_planes, s_w, s_drop, s_x,
-                            INJECT ? -1.0f : s_usel[idx], s_sel, s_ninc, s_pw, s_part[0]);
+      resident_eval<INJECT>(a, g, 0, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel, s_ninc, s_pw,
+                            s_part[0]);
   __syncthreads();
   prof_last = __builtin_amdgcn_s_memrealtime();
 
   for (int i = 0; i < a.N; ++i) {
     const uint64_t t = a.step0 + (uint64_t)i;
-    const float* inj = inj_of(i);
+    const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
     const int b3 = i % 3, b3n = (i + 1) % 3, b2 = i & 1, b2n = b2 ^ 1;
-    const uint32_t* xe = s_x + b3 * g.W;
+    // the sample's patch-major words, for the literal updates
+    const uint32_t* xe = g.P == 1 ? s_x + b3 * g.W : a.X + (int64_t)i * g.P * g.W;
     const bool more = i + 1 < a.N;
 
     // ---- B + C on wave 0; speculative A of sample i+1 and staging of i+2 on the others
@@ -657,12 +811,12 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     } else {
       if (more)
         for (int idx = wave - 1; idx < n_own; idx += nwv - 1)
-          resident_eval<INJECT>(a, g, inj_of(i + 1), c_begin, idx, t + 1, s_planes, s_w, s_drop, s_x + b3n * g.W,
-                                INJECT ? -1.0f : s_usel[b3n * cpw + idx], s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw,
-                                s_part[b2n]);
+          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel + b2n * cpw,
+                                s_ninc + b2n * cpw, s_pw, s_part[b2n]);
       if (i + 2 < a.N) {
         const int b3nn = (i + 2) % 3;
         stage_sample(a, g, i + 2, b3nn, s_x, s_y, threadIdx.x - kWave, blockDim.x - kWave);
+        if (g.P > 1) stage_xt(a, g, i + 2, b2, s_xt, threadIdx.x - kWave, blockDim.x - kWave);
         if (!INJECT)
           precompute_draws(a, g, i + 2, b3nn, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x - kWave,
                            blockDim.x - kWave);
@@ -682,10 +836,16 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
                                                 s_prob, s_w + idx * g.K, s_uq + ((int64_t)b3 * cpw + idx) * g.K,
                                                 s_uu + ((int64_t)b3 * cpw + idx) * g.K, s_drop[idx] != 0);
       if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
-      if (more && s_sel[b2n * cpw + idx] >= 0) {
+      const int spec_sel = more ? s_sel[b2n * cpw + idx] : -1;
+      if (spec_sel >= 0) {
         if (g.coalesced ? lane < g.K : lane == 0)
           atomicAdd((unsigned long long*)&s_part[b2n][kp], (unsigned long long)(-(long long)wold));
-        if (lane == 0) s_pw[idx] -= 1;
+        if (lane == 0) {
+          if (g.P == 1)
+            s_pw[idx] -= 1;
+          else
+            atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
+        }
       }
       if (lane == 0) {
         ++my_updates;
@@ -732,20 +892,18 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       __syncthreads();
     }
     YTM_PROF_MARK(4);
-    // D3: the owning wave applies each queued update, then evaluates the clause again on
-    // sample i+1 with its new state
-    for (int tk = 0; tk < ntask; ++tk) {
+    // D3: the waves apply the queued updates (round-robin), each then evaluating its clause
+    // again on sample i+1 with the new state
+    for (int tk = wave; tk < ntask; tk += nwv) {  // tasks round-robin over the waves
       const int idx = s_task_idx[tk];
-      if (idx % nwv != wave) continue;
       const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
       const int sb = s_task_sb[tk];
       const bool have = !INJECT && sb + __popcll(ops.m1a | ops.m1b) <= R;
       apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[b2 * cpw + idx], ops, s_planes + idx * cw, xe,
                         have ? s_rng + (int64_t)sb * g.W * (kPreGroups * 4) : nullptr);
       if (more)
-        resident_eval<INJECT>(a, g, inj_of(i + 1), c_begin, idx, t + 1, s_planes, s_w, s_drop, s_x + b3n * g.W,
-                              INJECT ? -1.0f : s_usel[b3n * cpw + idx], s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw,
-                              s_part[b2n]);
+        resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel + b2n * cpw,
+                              s_ninc + b2n * cpw, s_pw, s_part[b2n]);
     }
     YTM_PROF_MARK(5);
     __syncthreads();
@@ -754,7 +912,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   __syncthreads();
   for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) a.planes[c_begin * cw + j] = s_planes[j];
   for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) a.weights[c_begin * g.K + j] = s_w[j];
-  for (int64_t j = threadIdx.x; j < n_own; j += blockDim.x) a.patch_w[c_begin + j] = s_pw[j];
+  if (g.P == 1)
+    for (int64_t j = threadIdx.x; j < n_own; j += blockDim.x) a.patch_w[c_begin + j] = s_pw[j];
   if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
   if (threadIdx.x == 0) {
     atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);

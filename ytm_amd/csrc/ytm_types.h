@@ -14,7 +14,7 @@ using __hip_internal::uint64_t;
 
 namespace ytm {
 
-constexpr int kTrainThreads = 512;
+constexpr int kTrainThreads = 512;  // workgroup size of the built-in training kernels
 constexpr int kMaxPlanesHost = 16;  // must equal kMaxPlanes of ytm_device.h
 
 // Resolved model geometry and hyperparameters.  Listed once (X-macro) so that host code
@@ -49,6 +49,7 @@ constexpr int kMaxPlanesHost = 16;  // must equal kMaxPlanes of ytm_device.h
   X(double, s_inv)         /* typed S_INV widened to double */                                       \
   X(double, q_prob)        /* typed Q_PROB widened to double */                                      \
   X(uint32_t, s_thr)       /* floor(s_inv * 2^24) clamped to [0, 2^24] */                             \
+  X(int, threads)          /* training launch: threads per workgroup (0 outside training) */        \
   X(int, grid)             /* training launch: persistent workgroups (0 outside training) */         \
   X(int, group_size)       /* training launch: workgroups per class-sum group */                     \
   X(int, groups)           /* training launch: class-sum groups, ceil(grid / group_size) */
@@ -59,12 +60,22 @@ struct Geom {
 #undef YTM_GEOM_DECL
 };
 
+// Clauses of a model with several patches are evaluated on a literal-major copy of each
+// sample (one bitset over the patches per literal), when a bitset fits one 32-bit word per
+// wave lane.
+__host__ __device__ constexpr bool literal_major(const Geom& g) { return g.P > 1 && (g.P + 31) / 32 <= 64; }
+// The training kernel keeps the current literal-major sample in LDS when it fits 120 KiB.
+__host__ __device__ constexpr bool literal_major_lds(const Geom& g) {
+  return literal_major(g) && g.L * ((g.P + 31) / 32) * 4 <= 120 * 1024;
+}
+
 struct TrainArgs {
   uint32_t* planes;          // [C][np][W]
   float* weights;            // [C][K]
   int32_t* patch_w;          // [C][P]
   const float* bias;         // [K]
   const uint32_t* X;         // [N][P][W]  (first sample of this launch)
+  const uint32_t* XT;        // [N][L][ceil(P/32)] literal-major samples (literal_major(g)), or null
   const int32_t* Y;          // [N][K]
   const uint32_t* drop;      // [C]
   const float* inject;       // [N][inject_block] or nullptr
