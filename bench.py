@@ -167,7 +167,8 @@ def main() -> int:
             f"({st['last_fit_updates'] / N:.1f}/sample) workgroups {st['train_workgroups']} "
             f"kind {st['train_kind']} wait {st['last_fit_wait_frac']:.3f}")
         if os.environ.get("YTM_TRAIN_PROFILE"):
-            names = (("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier") if st["train_kind"] == 0
+            names = (("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier", "step1-slowest-wave")
+                     if st["train_kind"] == 0
                      else ("A", "barrier", "exchange", "barrier", "D", "barrier"))
             log("[bench]   phase us/sample (wave 0): "
                 + " ".join(f"{n} {v:.2f}" for n, v in zip(names, st["last_fit_phase_us"])))

@@ -73,7 +73,8 @@ typedef struct ytm_stats {
     double last_fit_phase_us[8]; /* with YTM_TRAIN_PROFILE=1: average microseconds per sample
                                     that wave 0 of each workgroup spends in each phase of the
                                     training kernel (resident: exchange, barrier, D1, barrier,
-                                    D2, D3, barrier; global: A, barrier, exchange, barrier, D,
+                                    D2, D3, barrier, and the slowest other wave's time in the
+                                    exchange step; global: A, barrier, exchange, barrier, D,
                                     barrier) */
 } ytm_stats;
 

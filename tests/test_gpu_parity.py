@@ -285,6 +285,33 @@ def test_pickle_roundtrip():
     np.testing.assert_array_equal(tm2.predict(Xt)[1], tm.predict(Xt)[1])
 
 
+def test_lzma_checkpoint_continue_training(tmp_path):
+    """A model saved the way the reference's examples save one (an LZMA-compressed pickle,
+    test/cutm/pneumonia_mnist/pneumonia_mnist.py:119-120), loaded and trained further,
+    matches the oracle restarted from the same state (unpickling re-runs __init__, which
+    restarts the random stream, base.py:555-558)."""
+    import lzma
+
+    tm, ref, X, y, Xt, yt = pair(3, 30, 10, clauses=20)
+    encX = tm.encode(X)
+    tm.fit(encX, y, is_X_encoded=True)
+    path = tmp_path / "model.tm"
+    with lzma.LZMAFile(path, "wb") as f:
+        pickle.dump(tm, f)
+    with lzma.LZMAFile(path, "rb") as f:
+        tm2 = pickle.load(f)  # written by this test
+    kw = dict(workloads.CONFIGS[3]["model"], number_of_clauses_per_class=20, seed=workloads.MODEL_SEED)
+    ref2 = orc.OracleTM(kw.pop("number_of_clauses_per_class"), kw.pop("T"), kw.pop("s"), kw.pop("dim"),
+                        kw.pop("n_classes"), **kw)
+    ref2.ta[:] = tm.get_ta_state().reshape(ref2.ta.shape)
+    ref2.w[:] = tm.get_weights().reshape(ref2.w.shape)
+    ref2.pw[:] = tm.get_patch_weights().reshape(ref2.pw.shape)
+    for _ in range(2):
+        tm2.fit(encX, y, is_X_encoded=True)
+        assert tm2.stats()["last_fit_updates"] == ref2.fit_encoded(encX, ref2.encode_y_multiclass(y))
+    assert_state_equal(tm2, ref2, "after the checkpoint")
+
+
 def test_multioutput():
     X, y, Xt, yt, kw = workloads.make(2, 150, 40)
     Y = np.stack([(y == k).astype(np.uint32) for k in range(10)], axis=1)

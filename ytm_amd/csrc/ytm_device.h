@@ -125,16 +125,53 @@ __device__ __forceinline__ void planes_dec(uint32_t* pl, int np, uint32_t m) {
 }
 
 // ---------------------------------------------------------------- wave64 helpers
-__device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+// Inclusive scans over the 64 lanes with DPP (data-parallel primitives: VALU operands read
+// from another lane), which avoid the LDS crossbar that lane shuffles go through: shifts by
+// 1, 2, 4, 8 within each row of 16 lanes (Hillis-Steele), then row_bcast:15 (lane 15 of
+// row r into row r+1, rows 1 and 3) and row_bcast:31 (lane 31 into rows 2 and 3).  A lane
+// whose source is out of range receives the identity.  Call with every lane active.
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+__device__ __forceinline__ int wave_scan_add_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr1, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr2, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr4, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr8, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast15, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast31, 0xc, 0xf, false);
   return v;
 }
 
-__device__ __forceinline__ int wave_max_i32(int v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off));
+__device__ __forceinline__ int wave_scan_max_i32(int v) {
+  const int lo = (int)0x80000000;
+  v = max(v, __builtin_amdgcn_update_dpp(lo, v, kDppRowShr1, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(lo, v, kDppRowShr2, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(lo, v, kDppRowShr4, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(lo, v, kDppRowShr8, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(lo, v, kDppRowBcast15, 0xa, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(lo, v, kDppRowBcast31, 0xc, 0xf, false));
   return v;
+}
+
+__device__ __forceinline__ uint32_t wave_scan_or_u32(uint32_t v) {
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr1, 0xf, 0xf, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr2, 0xf, 0xf, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr4, 0xf, 0xf, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowShr8, 0xf, 0xf, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowBcast15, 0xa, 0xf, false);
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowBcast31, 0xc, 0xf, false);
+  return v;
+}
+
+// Value of lane `src` (wave-uniform) in every lane.
+__device__ __forceinline__ int lane_value(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
+
+__device__ __forceinline__ int wave_sum_i32(int v) { return lane_value(wave_scan_add_i32(v), kWave - 1); }
+__device__ __forceinline__ int wave_max_i32(int v) { return lane_value(wave_scan_max_i32(v), kWave - 1); }
+__device__ __forceinline__ unsigned long long wave_or_u64(unsigned long long v) {
+  const uint32_t lo = wave_scan_or_u32((uint32_t)v), hi = wave_scan_or_u32((uint32_t)(v >> 32));
+  return ((unsigned long long)(uint32_t)lane_value((int)hi, kWave - 1) << 32) | (uint32_t)lane_value((int)lo, kWave - 1);
 }
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }

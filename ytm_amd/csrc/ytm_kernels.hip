@@ -394,8 +394,9 @@ int train_rng_slots(int cpw, const Geom& g) {
 }
 
 size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g) {
-  if (kind != TrainKind::kResident)  // sel, ninc [cpw]; the literal-major sample [L][PW]
-    return (size_t)2 * cpw * sizeof(int) + (literal_major_lds(g) ? (size_t)(g.L * ((g.P + 31) / 32)) * 4 : 0);
+  if (kind != TrainKind::kResident)  // task masks [cpw][3] u64; sel, ninc, task clause / slot [cpw]; sample [L][PW]
+    return (size_t)3 * cpw * 8 + (size_t)4 * cpw * sizeof(int) +
+           (literal_major_lds(g) ? (size_t)(g.L * ((g.P + 31) / 32)) * 4 : 0);
   // Resident kernel (layout of train_resident_body): task masks [cpw][3] u64; planes
   // [cpw][np][W]; weights [cpw][K]; samples [3][W]; sel, ninc [2][cpw]; drop, patch
   // weights [cpw]; targets [3][K]; bias [K]; rank-1 draws [3][cpw]; Q-skip and update

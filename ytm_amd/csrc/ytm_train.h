@@ -33,15 +33,7 @@ constexpr uint64_t kWaitTicks = 200000000ull;
 // resident kernel computes cooperatively ahead of applying an update.
 constexpr int kPreGroups = 3;
 
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int t = __shfl_up(v, off);
-    if (lane >= off) v += t;
-  }
-  return v;
-}
+__device__ __forceinline__ int wave_inclusive_scan(int v) { return wave_scan_add_i32(v); }
 
 // Literal-decrement mask of one (clause, class) update for the 32 literals of word w:
 // bit b set iff need bit b is set and u(literal 32w+b) <= S_INV.
@@ -116,8 +108,12 @@ __device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g,
         }
       }
     }
-    best = wave_max_i32(lb);
-    if (best > 0) break;
+    // lane q holds ranks 4(g0 - q) + 1 .. + 4, so the first lane with a hit has the best
+    const unsigned long long hit = __ballot(lb > 0);
+    if (hit) {
+      best = lane_value(lb, __ffsll((long long)hit) - 1);
+      break;
+    }
   }
   return best;
 }
@@ -152,19 +148,27 @@ __device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* in
     bool alive = true;
     for (int64_t wb = 0; wb < g.W && alive; wb += kWave) {
       // lane q holds mask word wb + q; lane j of each round of 64 finds the j-th included
-      // literal of the chunk (binary search over the prefix counts, then a select)
+      // literal of the chunk (a walk over the words' prefix counts, then a select)
       const uint32_t mv = wb + lane < g.W ? m[wb + lane] : 0u;
       const int pc = __popc(mv);
       const int incl = wave_inclusive_scan(pc);
-      const int tot = __shfl(incl, kWave - 1);
+      const int tot = lane_value(incl, kWave - 1);
+      const int nw = (int)(g.W - wb < kWave ? g.W - wb : kWave);
       for (int jb = 0; jb < tot && alive; jb += kWave) {
         const int j = jb + lane;
-        int q = 0;  // first lane whose inclusive count exceeds j
-#pragma unroll
-        for (int step = kWave / 2; step > 0; step >>= 1)
-          if (__shfl(incl, q + step - 1) <= j) q += step;
-        const uint32_t mw = __shfl(mv, q);
-        int r = j - (__shfl(incl, q) - __shfl(pc, q));  // rank of the literal within word q
+        // the word holding literal j: walk the chunk's words (their counts read as scalars)
+        uint32_t mw = 0u;
+        int q = 0, ex = 0, before = 0;
+        for (int w = 0; w < nw; ++w) {
+          const int after = lane_value(incl, w);
+          if (before <= j && j < after) {
+            q = w;
+            ex = before;
+            mw = (uint32_t)lane_value((int)mv, w);
+          }
+          before = after;
+        }
+        int r = j - ex;  // rank of the literal within word q
         uint32_t v = mw;
         int pos = 0;
 #pragma unroll
@@ -197,7 +201,7 @@ __device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* in
   }
   const int pc = lane < PW ? __popc(acc) : 0;
   const int incl = wave_inclusive_scan(pc);
-  const int R = __shfl(incl, kWave - 1);
+  const int R = lane_value(incl, kWave - 1);
   if (R == 0) return -1;
   const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R);
   if (best == 0) return -1;
@@ -212,7 +216,7 @@ __device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* in
     for (int q = 1; q < best - excl; ++q) v &= v - 1u;
     pos = src * 32 + __builtin_ctz(v);
   }
-  return __shfl(pos, src);
+  return lane_value(pos, src);
 }
 
 // Phase A for one clause (wave-uniform): returns the selected patch or -1 and the
@@ -293,7 +297,7 @@ __device__ int eval_select(const TrainArgs& a, const Geom& g, const float* inj, 
       for (int q = 1; q < best - excl; ++q) v &= v - 1ull;
       pos = src * kWave + __ffsll((long long)v) - 1;
     }
-    return __shfl(pos, src);
+    return lane_value(pos, src);
   }
 }
 
@@ -399,16 +403,77 @@ __device__ void apply_ops(const TrainArgs& a, const Geom& g, const float* inj, i
   }
 }
 
-// Phase D for one non-dropped clause.  Returns true when any Type Ia/Ib/II branch ran.
-// cplanes: the clause's np planes (stride W), wrow: its K weights, xe: the sample.
+// Tasks per wave when ntask queued clause updates are spread over nwv waves, at most
+// 64 / W of them packed into one wave: spread first, pack only what is left over.
+__device__ __forceinline__ int tasks_per_wave(const Geom& g, int ntask, int nwv) {
+  const int cap = kWave / (int)g.W;
+  const int even = (ntask + nwv - 1) / nwv;
+  return even < 1 ? 1 : (even > cap ? cap : even);
+}
+
+// Literal updates of several queued clauses at once, for models whose clauses have at most
+// 32 literal words: lanes [g*W, g*W + W) of the wave take task tk0 + g (g < per <= 64 / W).
+// Per class in increasing k, every clause with a feedback branch at that class applies it
+// exactly as apply_ops does.  Tasks: clause s_task_idx[tk], masks s_task_m[tk][3] (bits
+// relative to the clause's first class), first draw slot s_task_sb[tk] (s_rng null: draws
+// computed here); sel_of[idx] the clause's selected patch; planes of clause idx at
+// planes_base + idx * np * W; xe the sample's patch-major words.
 template <bool INJECT>
-__device__ bool feedback(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, int sel, int ninc,
-                         const int* s_tgt, const double* s_prob, uint32_t* cplanes, float* wrow,
-                         const uint32_t* xe, const float* pre_uq, const float* pre_uu) {
-  const FbOps ops = decide<INJECT, false>(a, g, inj, c, t, sel, ninc, s_tgt, s_prob, wrow, pre_uq, pre_uu);
-  if ((ops.m1a | ops.m1b | ops.m2) == 0ull) return false;
-  apply_ops<INJECT>(a, g, inj, c, t, sel, ops, cplanes, xe, nullptr);
-  return true;
+__device__ void apply_tasks(const TrainArgs& a, const Geom& g, const float* inj, int64_t c_begin, uint64_t t, int tk0,
+                            int per, int ntask, const int* s_task_idx, const unsigned long long* s_task_m,
+                            const int* s_task_sb, const int* sel_of, uint32_t* planes_base, const uint32_t* xe,
+                            const uint32_t* s_rng, int R) {
+  const int lane = lane_id();
+  const int W = (int)g.W;
+  const int grp = lane / W, w = lane % W;
+  const int tk = tk0 + grp;
+  const bool act = grp < per && tk < ntask;
+  int idx = 0, sb = 0, sel = -1;
+  unsigned long long m1a = 0ull, m1b = 0ull, m2 = 0ull;
+  if (act) {
+    idx = s_task_idx[tk];
+    m1a = s_task_m[tk * 3 + 0];
+    m1b = s_task_m[tk * 3 + 1];
+    m2 = s_task_m[tk * 3 + 2];
+    sb = s_task_sb[tk];
+    sel = sel_of[idx];
+  }
+  const int64_t c = c_begin + idx;
+  const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+  const int np = g.np;
+  const uint32_t F = act ? (w == W - 1 ? g.last_filter : 0xFFFFFFFFu) : 0u;
+  uint32_t* pw = planes_base + (int64_t)idx * np * W + w;
+  uint32_t pl[kMaxPlanes];
+#pragma unroll
+  for (int j = 0; j < kMaxPlanes; ++j) pl[j] = (j < np && act) ? pw[(int64_t)j * W] : 0u;
+  const uint32_t xb = (act && sel >= 0) ? xe[(int64_t)sel * W + w] : 0u;
+  const unsigned long long t1 = m1a | m1b;
+  const bool have = s_rng != nullptr && act && sb + __popcll(t1) <= R;
+  unsigned long long u = wave_or_u64(m1a | m1b | m2);  // union of the wave's class bits
+  int rng_op = 0;
+  while (u) {
+    const int b = __ffsll((long long)u) - 1;
+    u &= u - 1ull;
+    const int64_t k = kb + b;
+    const bool is1 = (t1 >> b) & 1ull, is1a = (m1a >> b) & 1ull, is2 = (m2 >> b) & 1ull;
+    if (__any(is1)) {
+      // Type Ia (kernel.cu:410-443) / Type Ib (kernel.cu:453-470)
+      const uint32_t pos = planes_gt(pl, np, g.off) & F;
+      const uint32_t need = is1 ? (is1a ? (~xb & pos) : pos) : 0u;
+      const uint32_t* pre_w = have ? s_rng + ((int64_t)(sb + rng_op) * W + w) * (kPreGroups * 4) : nullptr;
+      const uint32_t dec = literal_draw_mask<INJECT>(a, g, inj, need, t, c, k, w, pre_w, have);
+      planes_inc(pl, np, is1a ? (xb & planes_lt(pl, np, g.max_state_p) & F) : 0u);
+      planes_dec(pl, np, dec);
+      if (is1) ++rng_op;
+    }
+    // Type II (kernel.cu:481-506): literal 0 -> +1, no upper guard.
+    if (__any(is2)) planes_inc(pl, np, is2 ? (~xb & F) : 0u);
+  }
+  if (act) {
+#pragma unroll
+    for (int j = 0; j < kMaxPlanes; ++j)
+      if (j < np) pw[(int64_t)j * W] = pl[j];
+  }
 }
 
 // Phases B and C, run by wave 0 of every workgroup.  Per sample, a two-level all-reduce
@@ -526,9 +591,14 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   const int G = gridDim.x, wg = blockIdx.x;
   const int64_t c_begin = g.C * wg / G, c_end = g.C * (wg + 1) / G;
   const int n_own = (int)(c_end - c_begin);
-  int* s_sel = (int*)dyn_lds;                          // [cpw]
-  int* s_ninc = s_sel + a.cpw;                         // [cpw]
-  uint32_t* s_xt = (uint32_t*)(s_ninc + a.cpw);        // [L][PW] when literal_major_lds(g)
+  __shared__ int s_ntask;
+  unsigned long long* s_task_m = (unsigned long long*)dyn_lds;  // [cpw][3] feedback masks
+  int* s_sel = (int*)(s_task_m + 3 * a.cpw);                   // [cpw]
+  int* s_ninc = s_sel + a.cpw;                                 // [cpw]
+  int* s_task_idx = s_ninc + a.cpw;                            // [cpw]
+  int* s_task_sb = s_task_idx + a.cpw;                         // [cpw] (zero: no precomputed draws)
+  uint32_t* s_xt = (uint32_t*)(s_task_sb + a.cpw);             // [L][PW] when literal_major_lds(g)
+  const int64_t cw = (int64_t)g.np * g.W;
   const int64_t xt_words = literal_major(g) ? g.L * ((g.P + 31) / 32) : 0;
   unsigned long long my_updates = 0ull;
   uint64_t wait_ticks = 0;
@@ -564,7 +634,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     for (;;) {
       int idx = 0;
       if (lane == 0) idx = atomicAdd(&s_next, 1);
-      idx = __shfl(idx, 0);
+      idx = lane_value(idx, 0);
       if (idx >= n_own) break;
       const int64_t c = c_begin + idx;
       int ninc;
@@ -589,22 +659,49 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     if (wave == 0)
       exchange_class_sums(a, g, i, a.Y + (int64_t)i * g.K, a.bias, s_part, s_tgt, s_prob, &s_abort, &wait_ticks);
     YTM_PROF_MARK(2);
-    if (threadIdx.x == 0) s_next = 0;
+    if (threadIdx.x == 0) {
+      s_next = 0;
+      s_ntask = 0;
+    }
     __syncthreads();
     YTM_PROF_MARK(3);
     if (s_abort) break;
 
-    // ---- D: feedback
+    // ---- D: feedback.  Decisions (weights updated in place) per clause, claimed
+    // dynamically; narrow clauses (W <= 32) are queued and their literal updates packed
+    // several to a wave, wide ones are updated right away by the deciding wave.
     for (;;) {
       int idx = 0;
       if (lane == 0) idx = atomicAdd(&s_next, 1);
-      idx = __shfl(idx, 0);
+      idx = lane_value(idx, 0);
       if (idx >= n_own) break;
       const int64_t c = c_begin + idx;
       if (a.drop[c] == 1u) continue;
-      const bool touched = feedback<INJECT>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob,
-                                            a.planes + c * g.np * g.W, a.weights + c * g.K, xe, nullptr, nullptr);
-      if (touched && lane == 0) ++my_updates;
+      const FbOps ops = decide<INJECT, false>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob,
+                                              a.weights + c * g.K, nullptr, nullptr);
+      if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
+      if (lane == 0) ++my_updates;
+      if (g.W <= 32) {
+        if (lane == 0) {
+          const int tk = atomicAdd(&s_ntask, 1);
+          s_task_idx[tk] = idx;
+          s_task_sb[tk] = 0;
+          s_task_m[tk * 3 + 0] = ops.m1a;
+          s_task_m[tk * 3 + 1] = ops.m1b;
+          s_task_m[tk * 3 + 2] = ops.m2;
+        }
+      } else {
+        apply_ops<INJECT>(a, g, inj, c, t, s_sel[idx], ops, a.planes + c * cw, xe, nullptr);
+      }
+    }
+    if (g.W <= 32) {
+      __syncthreads();
+      const int ntask = s_ntask;
+      const int nwv = (int)(blockDim.x / kWave);
+      const int per = tasks_per_wave(g, ntask, nwv);
+      for (int tk0 = wave * per; tk0 < ntask; tk0 += nwv * per)
+        apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb, s_sel,
+                            a.planes + c_begin * cw, xe, nullptr, 0);
     }
     YTM_PROF_MARK(4);
     __syncthreads();
@@ -728,6 +825,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   __shared__ double s_prob[64];
   __shared__ int s_abort;
   __shared__ int s_ntask, s_nslot;
+  __shared__ unsigned long long s_spec_max;  // profile: slowest wave's time in step 1 (waves >= 1)
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int nwv = blockDim.x / kWave;  // >= 2 (kTrainThreads)
@@ -782,7 +880,9 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     s_abort = 0;
     s_ntask = 0;
     s_nslot = 0;
+    s_spec_max = 0ull;
   }
+  uint64_t spec_ticks = 0;  // profile: this wave's time in step 1 (waves >= 1)
   __syncthreads();
   // Phase A of sample 0, every wave.
   if (a.N > 0)
@@ -809,6 +909,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       exchange_class_sums(a, g, i, s_y + b3 * g.K, s_bias, s_part[b2], s_tgt, s_prob, &s_abort, &wait_ticks);
       YTM_PROF_MARK(0);
     } else {
+      const uint64_t spec_t0 = a.profile ? __builtin_amdgcn_s_memrealtime() : 0;
       if (more)
         for (int idx = wave - 1; idx < n_own; idx += nwv - 1)
           resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel + b2n * cpw,
@@ -821,6 +922,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
           precompute_draws(a, g, i + 2, b3nn, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x - kWave,
                            blockDim.x - kWave);
       }
+      if (a.profile) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
     }
     __syncthreads();
     YTM_PROF_MARK(1);
@@ -894,16 +996,29 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     YTM_PROF_MARK(4);
     // D3: the waves apply the queued updates (round-robin), each then evaluating its clause
     // again on sample i+1 with the new state
-    for (int tk = wave; tk < ntask; tk += nwv) {  // tasks round-robin over the waves
-      const int idx = s_task_idx[tk];
-      const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
-      const int sb = s_task_sb[tk];
-      const bool have = !INJECT && sb + __popcll(ops.m1a | ops.m1b) <= R;
-      apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[b2 * cpw + idx], ops, s_planes + idx * cw, xe,
-                        have ? s_rng + (int64_t)sb * g.W * (kPreGroups * 4) : nullptr);
-      if (more)
-        resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel + b2n * cpw,
-                              s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+    if (g.W <= 32) {
+      // narrow clauses: up to 64 / W tasks per wave at once
+      const int per = tasks_per_wave(g, ntask, nwv);
+      for (int tk0 = wave * per; tk0 < ntask; tk0 += nwv * per) {
+        apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb,
+                            s_sel + b2 * cpw, s_planes, xe, INJECT ? nullptr : s_rng, R);
+        if (more)
+          for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk)
+            resident_eval<INJECT>(a, g, i + 1, c_begin, s_task_idx[tk], s_planes, s_w, s_drop, s_x, s_xt, s_usel,
+                                  s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+      }
+    } else {
+      for (int tk = wave; tk < ntask; tk += nwv) {  // tasks round-robin over the waves
+        const int idx = s_task_idx[tk];
+        const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
+        const int sb = s_task_sb[tk];
+        const bool have = !INJECT && sb + __popcll(ops.m1a | ops.m1b) <= R;
+        apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[b2 * cpw + idx], ops, s_planes + idx * cw, xe,
+                          have ? s_rng + (int64_t)sb * g.W * (kPreGroups * 4) : nullptr);
+        if (more)
+          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel + b2n * cpw,
+                                s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+      }
     }
     YTM_PROF_MARK(5);
     __syncthreads();
@@ -915,11 +1030,15 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   if (g.P == 1)
     for (int64_t j = threadIdx.x; j < n_own; j += blockDim.x) a.patch_w[c_begin + j] = s_pw[j];
   if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
+  if (a.profile && lane == 0 && wave > 0) atomicMax(&s_spec_max, (unsigned long long)spec_ticks);
+  __syncthreads();
   if (threadIdx.x == 0) {
     atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
     atomicAdd(&a.counters[2], (unsigned long long)(__builtin_amdgcn_s_memrealtime() - t_kernel));
-    if (prof)
+    if (prof) {
+      prof_acc[7] = s_spec_max;  // slot 7: the workgroup's slowest wave in step 1
       for (int j = 0; j < 8; ++j) atomicAdd(&a.counters[4 + j], (unsigned long long)prof_acc[j]);
+    }
   }
 }
 
