@@ -251,6 +251,72 @@ __global__ __launch_bounds__(256) void score_kernel(const uint32_t* __restrict__
   }
 }
 
+// One patch: lanes are samples.  A block takes a tile of 64 samples (staged transposed in
+// LDS, [W][64], so that lane e reads word w of its own sample) and a chunk of clauses; each
+// wave walks its clauses, reading a clause's mask words once and skipping the zero ones with
+// scalar logic, so one instruction tests a mask word against 64 samples.  A lane whose
+// sample the clause fires on adds the clause's weights to its int64 sums, which go to the
+// exact accumulators at the end of the chunk (calc_class_sums_infer_batch, kernel.cu:319-343:
+// empty clauses do not vote).
+constexpr int kScoreTile = 64;
+constexpr int kScoreTileChunk = 256;
+constexpr int kScoreTileMaxK = 16;
+
+__global__ __launch_bounds__(256) void score_tile_kernel(const uint32_t* __restrict__ planes,
+                                                         const int32_t* __restrict__ ninc,
+                                                         const float* __restrict__ w,
+                                                         const uint32_t* __restrict__ X, int64_t N, Geom g,
+                                                         long long* __restrict__ acc) {
+  extern __shared__ uint32_t s_tile[];  // [W][64]
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave, nwv = blockDim.x / kWave;
+  const int64_t ntile = (N + kScoreTile - 1) / kScoreTile;
+  const int64_t nch = (g.C + kScoreTileChunk - 1) / kScoreTileChunk;
+  for (int64_t blk = blockIdx.x; blk < ntile * nch; blk += gridDim.x) {
+    const int64_t e0 = (blk / nch) * kScoreTile, ch = blk % nch;
+    const int64_t c0 = ch * kScoreTileChunk;
+    const int64_t c1 = c0 + kScoreTileChunk < g.C ? c0 + kScoreTileChunk : g.C;
+    __syncthreads();  // the previous tile is no longer read
+    for (int64_t j = threadIdx.x; j < kScoreTile * g.W; j += blockDim.x) {
+      const int64_t sidx = j / g.W, ww = j % g.W, e = e0 + sidx;
+      s_tile[ww * kScoreTile + sidx] = e < N ? X[e * g.W + ww] : 0u;
+    }
+    __syncthreads();
+    long long sum[kScoreTileMaxK];
+#pragma unroll
+    for (int k = 0; k < kScoreTileMaxK; ++k) sum[k] = 0;
+    for (int64_t c = c0 + wave; c < c1; c += nwv) {
+      if (ninc[c] == 0) continue;  // empty clauses do not vote
+      const uint32_t* m = planes + (c * g.np + g.np - 1) * g.W;
+      bool alive = true;
+      for (int64_t wb = 0; wb < g.W; wb += kWave) {
+        const uint32_t mv = wb + lane < g.W ? m[wb + lane] : 0u;
+        unsigned long long nz = __ballot(mv != 0u);  // the chunk's non-zero mask words
+        int tested = 0;
+        while (nz) {
+          const int q = __ffsll((long long)nz) - 1;
+          nz &= nz - 1ull;
+          const uint32_t mw = (uint32_t)lane_value((int)mv, q);
+          alive = alive && (mw & ~s_tile[(wb + q) * kScoreTile + lane]) == 0u;
+          if ((++tested & 7) == 0 && !__any(alive)) break;
+        }
+        if (!__any(alive)) break;
+      }
+      if (alive) {
+#pragma unroll
+        for (int k = 0; k < kScoreTileMaxK; ++k)
+          if (k < g.K) sum[k] += (long long)w[c * g.K + k];
+      }
+    }
+    const int64_t e = e0 + lane;
+    if (e < N) {
+#pragma unroll
+      for (int k = 0; k < kScoreTileMaxK; ++k)
+        if (k < g.K && sum[k] != 0) atomicAdd((unsigned long long*)&acc[e * g.K + k], (unsigned long long)sum[k]);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void score_finish_kernel(const long long* __restrict__ acc,
                                                            const float* __restrict__ bias, int64_t N,
                                                            Geom g, float* __restrict__ out) {
@@ -355,6 +421,12 @@ hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s) {
 
 hipError_t launch_score(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
                         int64_t N, const Geom& g, long long* acc, hipStream_t s) {
+  if (g.P == 1 && g.K <= kScoreTileMaxK && (size_t)g.W * kScoreTile * 4 <= 48 * 1024) {
+    const int64_t blocks = ((N + kScoreTile - 1) / kScoreTile) * ((g.C + kScoreTileChunk - 1) / kScoreTileChunk);
+    const int grid = blocks < 65536 ? (int)blocks : 65536;
+    score_tile_kernel<<<grid, 256, (size_t)g.W * kScoreTile * 4, s>>>(planes, ninc, w, X, N, g, acc);
+    return hipGetLastError();
+  }
   const int64_t blocks = N * ((g.C + kScoreChunk - 1) / kScoreChunk);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
   if (g.P == 1)
