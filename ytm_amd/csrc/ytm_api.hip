@@ -173,6 +173,35 @@ Geom train_geometry(const Geom& model, int cus, int* cpw) {
   return g;
 }
 
+bool train_lds_fits(const Geom& g, ytm::TrainKind kind, int cpw, int cap) {
+  Geom gc = g;
+  gc.list_cap = cap;
+  const int r = kind == ytm::TrainKind::kResident ? ytm::train_rng_slots(cpw, gc) : 0;
+  return ytm::train_lds_bytes(kind, cpw, r, gc) <= kResidentLdsLimit;
+}
+
+// Literal-list capacity of a training kernel kind (several patches): the resident kernel
+// keeps 64 per clause, the global one the largest of 256..64 that fits; 0 when none fits.
+int train_list_cap(const Geom& g, ytm::TrainKind kind, int cpw) {
+  if (!ytm::literal_major(g) || g.L > 65535) return 0;
+  if (kind == ytm::TrainKind::kResident) return train_lds_fits(g, kind, cpw, 64) ? 64 : 0;
+  for (int cap : {256, 192, 128, 64})
+    if (train_lds_fits(g, kind, cpw, cap)) return cap;
+  return 0;
+}
+
+// Keeps the workgroup's clause state resident in LDS when it fits (with several patches,
+// together with two literal-major samples), else the global kernel; sets g->list_cap.
+ytm::TrainKind choose_train_kind(Geom* g, int cpw, bool force_global) {
+  ytm::TrainKind kind = g->P == 1 ? ytm::TrainKind::kGlobalVanilla : ytm::TrainKind::kGlobalConv;
+  if (!force_global && (g->P == 1 || ytm::literal_major(*g))) {
+    const int cap = train_list_cap(*g, ytm::TrainKind::kResident, cpw);
+    if (train_lds_fits(*g, ytm::TrainKind::kResident, cpw, cap)) kind = ytm::TrainKind::kResident;
+  }
+  g->list_cap = train_list_cap(*g, kind, cpw);
+  return kind;
+}
+
 }  // namespace
 
 extern "C" {
@@ -248,10 +277,11 @@ int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injec
   int rc = resolve_geometry(*params, &model);
   if (rc) return rc;
   int cpw;
-  const Geom g = train_geometry(model, compute_units > 0 ? compute_units : 256, &cpw);
+  Geom g = train_geometry(model, compute_units > 0 ? compute_units : 256, &cpw);
   const bool valid = train_kind == 1 ? g.P == 1 : train_kind == 2 ? g.P > 1 : (g.P == 1 || ytm::literal_major(g));
   if (!valid)
     return fail(YTM_EINVAL, "train_kind 1 is for one patch, 2 for several, 0 for one patch or a literal-major model");
+  g.list_cap = train_list_cap(g, (ytm::TrainKind)train_kind, cpw);
   std::vector<char> code;
   std::string why;
   if (!ytm::jit_compile(g, (ytm::TrainKind)train_kind, injected != 0, &code, &why))
@@ -365,13 +395,8 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   Geom g = train_geometry(m->g, m->cus, &cpw);  // the training kernels read both
   const int grid = g.grid, D = g.groups;
   const bool inj = inject != nullptr;
-  // Keep the workgroup's clause state resident in LDS when it fits (with several patches,
-  // together with two literal-major samples).
-  ytm::TrainKind kind = g.P == 1 ? ytm::TrainKind::kGlobalVanilla : ytm::TrainKind::kGlobalConv;
   const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
-  if ((g.P == 1 || ytm::literal_major(g)) && !(force_global && std::atoi(force_global) > 0) &&
-      ytm::train_lds_bytes(ytm::TrainKind::kResident, cpw, ytm::train_rng_slots(cpw, g), g) <= kResidentLdsLimit)
-    kind = ytm::TrainKind::kResident;
+  const ytm::TrainKind kind = choose_train_kind(&g, cpw, force_global && std::atoi(force_global) > 0);
   const int rng_slots = kind == ytm::TrainKind::kResident ? ytm::train_rng_slots(cpw, g) : 0;
   const size_t lds = ytm::train_lds_bytes(kind, cpw, rng_slots, g);
   // Kernel specialised for this model's geometry (hipRTC), else the built-in one.

@@ -466,8 +466,11 @@ int train_rng_slots(int cpw, const Geom& g) {
 }
 
 size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g) {
+  // literal lists (several patches): include counts [cpw, rounded to even] and lists [cpw][cap] u16
+  const size_t cap = g.P > 1 ? (size_t)g.list_cap : 0;
+  const size_t lists = cap > 0 ? (size_t)2 * ((cpw + 1) / 2) * 4 + (size_t)cpw * cap * 2 : 0;
   if (kind != TrainKind::kResident)  // task masks [cpw][3] u64; sel, ninc, task clause / slot [cpw]; sample [L][PW]
-    return (size_t)3 * cpw * 8 + (size_t)4 * cpw * sizeof(int) +
+    return (size_t)3 * cpw * 8 + (size_t)4 * cpw * sizeof(int) + lists +
            (literal_major_lds(g) ? (size_t)(g.L * ((g.P + 31) / 32)) * 4 : 0);
   // Resident kernel (layout of train_resident_body): task masks [cpw][3] u64; planes
   // [cpw][np][W]; weights [cpw][K]; samples [3][W]; sel, ninc [2][cpw]; drop, patch
@@ -477,7 +480,7 @@ size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g) {
   // Several patches add the literal-major samples [2][L][PW] after the task masks.
   const size_t C = (size_t)cpw, K = (size_t)g.K, W = (size_t)g.W, R = (size_t)rng_slots;
   const size_t xt = g.P > 1 ? (size_t)(2 * g.L * ((g.P + 31) / 32)) * 4 : 0;
-  return 3 * C * 8 + xt + C * (size_t)g.np * W * 4 + C * K * 4 + 3 * W * 4 + 4 * C * 4 + 2 * C * 4 + 3 * K * 4 +
+  return 3 * C * 8 + lists + xt + C * (size_t)g.np * W * 4 + C * K * 4 + 3 * W * 4 + 4 * C * 4 + 2 * C * 4 + 3 * K * 4 +
          K * 4 + 3 * C * 4 + 6 * C * K * 4 + 2 * C * 4 + 2 * R * 4 + R * W * kPreGroups * 4 * 4;
 }
 

@@ -118,94 +118,20 @@ __device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g,
   return best;
 }
 
-// Phase A for one clause of a model with several patches, on the literal-major sample xt
-// ([L][PW] words, PW = ceil(P/32) <= 64; bit b of word j of literal l: literal l set in
-// patch 32j + b).  The clause fires on the patches where every included literal is set,
-// so its firing bitmap is the AND of its included literals' bitsets (fast_eval,
-// kernel.cu:255-282): lane j keeps patch word j, the included literals are walked 8 at a
-// time (a short batch repeats its last literal, AND being idempotent) and the walk stops
-// once no patch can fire.  Then the reservoir choice as in eval_select.  Wave-uniform.
+// Patch of a clause with several patches from its firing bitmap (lane j: patch word j,
+// j < PW): reservoir rank among the R firing patches, then the patch of that rank.
+// Returns -1 when none is selected.  Wave-uniform.
 template <bool INJECT>
-__device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, const uint32_t* m,
-                              const uint32_t* xt, bool dropped, int* ninc_out) {
+__device__ __forceinline__ int select_from_bitmap(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t,
+                                                  uint32_t acc) {
   const int lane = lane_id();
-  const bool exact_count = g.maxinc < g.L;
   const int PW = (int)((g.P + 31) / 32);
-  int cnt = 0;
-  uint32_t any = 0u;
-  for (int64_t w = lane; w < g.W; w += kWave) {
-    const uint32_t mw = m[w];
-    if (exact_count) cnt += __popc(mw);
-    any |= mw;
-  }
-  const int ninc = exact_count ? wave_sum_i32(cnt) : (__any(any != 0u) ? 1 : 0);
-  *ninc_out = ninc;
-  if (dropped) return -1;
-  uint32_t acc = 0u;
-  if (lane < PW) acc = (lane == PW - 1 && (g.P & 31)) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu;
-  if (ninc != 0) {  // an empty clause fires on every patch in training
-    const int jl = lane < PW ? lane : 0;
-    bool alive = true;
-    for (int64_t wb = 0; wb < g.W && alive; wb += kWave) {
-      // lane q holds mask word wb + q; lane j of each round of 64 finds the j-th included
-      // literal of the chunk (a walk over the words' prefix counts, then a select)
-      const uint32_t mv = wb + lane < g.W ? m[wb + lane] : 0u;
-      const int pc = __popc(mv);
-      const int incl = wave_inclusive_scan(pc);
-      const int tot = lane_value(incl, kWave - 1);
-      const int nw = (int)(g.W - wb < kWave ? g.W - wb : kWave);
-      for (int jb = 0; jb < tot && alive; jb += kWave) {
-        const int j = jb + lane;
-        // the word holding literal j: walk the chunk's words (their counts read as scalars)
-        uint32_t mw = 0u;
-        int q = 0, ex = 0, before = 0;
-        for (int w = 0; w < nw; ++w) {
-          const int after = lane_value(incl, w);
-          if (before <= j && j < after) {
-            q = w;
-            ex = before;
-            mw = (uint32_t)lane_value((int)mv, w);
-          }
-          before = after;
-        }
-        int r = j - ex;  // rank of the literal within word q
-        uint32_t v = mw;
-        int pos = 0;
-#pragma unroll
-        for (int width = 16; width > 0; width >>= 1) {
-          const int lowc = __popc(v & ((1u << width) - 1u));
-          if (r >= lowc) {
-            r -= lowc;
-            v >>= width;
-            pos += width;
-          }
-        }
-        const int lit = (int)(32 * (wb + q)) + pos;  // valid for lanes j < tot
-        const int cnt = tot - jb < kWave ? tot - jb : kWave;
-        for (int jj = 0; jj < cnt; jj += 8) {
-          uint32_t vv = 0xFFFFFFFFu;
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            // a short last batch repeats literal jj (AND is idempotent)
-            const int l = __builtin_amdgcn_readlane(lit, jj + u < cnt ? jj + u : jj);
-            vv &= xt[l * PW + jl];
-          }
-          acc &= vv;
-          if (((jj >> 3) & 1) && !__any(acc != 0u)) {  // every 16 literals: stop once nothing fires
-            alive = false;
-            break;
-          }
-        }
-      }
-    }
-  }
   const int pc = lane < PW ? __popc(acc) : 0;
   const int incl = wave_inclusive_scan(pc);
   const int R = lane_value(incl, kWave - 1);
   if (R == 0) return -1;
   const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R);
   if (best == 0) return -1;
-  // Patch of the best-th set bit of the firing bitmap.
   const int excl = incl - pc;
   const bool here = lane < PW && best > excl && best <= incl;
   const unsigned long long hb = __ballot(here);
@@ -217,6 +143,183 @@ __device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* in
     pos = src * 32 + __builtin_ctz(v);
   }
   return lane_value(pos, src);
+}
+
+// All-ones firing bitmap word of lane j (patches 32j .. 32j+31 that exist), 0 beyond PW.
+__device__ __forceinline__ uint32_t all_patches_word(const Geom& g) {
+  const int lane = lane_id();
+  const int PW = (int)((g.P + 31) / 32);
+  if (lane >= PW) return 0u;
+  return (lane == PW - 1 && (g.P & 31)) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu;
+}
+
+// Included literals of a clause (include mask m, W words), in increasing order, written to
+// list[0, n) when n <= cap, the entries from n to the next multiple of 8 repeating literal
+// n-1 (cap a multiple of 8).  Returns n, the include count.  Lane j of each round of 64
+// finds the j-th included literal: the word holding it from a walk over the words' prefix
+// counts, then its bit by a select.  Wave-uniform.
+__device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* list, int cap) {
+  const int lane = lane_id();
+  int total = 0, last = 0;
+  for (int64_t wb = 0; wb < g.W; wb += kWave) {
+    const uint32_t mv = wb + lane < g.W ? m[wb + lane] : 0u;
+    const int pc = __popc(mv);
+    const int incl = wave_inclusive_scan(pc);
+    const int tot = lane_value(incl, kWave - 1);
+    const int nw = (int)(g.W - wb < kWave ? g.W - wb : kWave);
+    for (int jb = 0; jb < tot; jb += kWave) {
+      const int j = jb + lane;
+      uint32_t mw = 0u;
+      int q = 0, ex = 0, before = 0;
+      for (int w = 0; w < nw; ++w) {
+        const int after = lane_value(incl, w);
+        if (before <= j && j < after) {
+          q = w;
+          ex = before;
+          mw = (uint32_t)lane_value((int)mv, w);
+        }
+        before = after;
+      }
+      int r = j - ex, pos = 0;
+      uint32_t v = mw;
+#pragma unroll
+      for (int width = 16; width > 0; width >>= 1) {
+        const int lowc = __popc(v & ((1u << width) - 1u));
+        if (r >= lowc) {
+          r -= lowc;
+          v >>= width;
+          pos += width;
+        }
+      }
+      const int lit = (int)(32 * (wb + q)) + pos;
+      const int cnt = tot - jb < kWave ? tot - jb : kWave;
+      if (j < tot && total + j < cap) list[total + j] = (uint16_t)lit;
+      last = lane_value(lit, cnt - 1);
+    }
+    total += tot;
+  }
+  if (total > 0 && total <= cap) {
+    const int pad_end = ((total + 7) & ~7) < cap ? ((total + 7) & ~7) : cap;
+    for (int p = total + lane; p < pad_end; p += kWave) list[p] = (uint16_t)last;
+  }
+  return total;
+}
+
+// Firing bitmap of a clause from its literal list (n literals, padded to a multiple of 8)
+// on the literal-major sample xt: acc AND-ed with the bitsets of the listed literals, 8 per
+// step (two 8-byte reads of the list, the same for every lane); stops once nothing fires.
+// list must be 8-byte aligned.
+__device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16_t* list, int n, const uint32_t* xt,
+                                                     uint32_t acc) {
+  const int lane = lane_id();
+  const int PW = (int)((g.P + 31) / 32);
+  const int jl = lane < PW ? lane : 0;
+  for (int j = 0; j < n; j += 8) {
+    const uint2 q0 = *(const uint2*)(list + j), q1 = *(const uint2*)(list + j + 4);
+    const uint32_t w8[4] = {q0.x, q0.y, q1.x, q1.y};
+    uint32_t v = 0xFFFFFFFFu;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)jl];
+      v &= xt[(w8[u] >> 16) * (uint32_t)PW + (uint32_t)jl];
+    }
+    acc &= v;
+    if ((j & 8) && !__any(acc != 0u)) break;  // every 16 literals: stop once nothing fires
+  }
+  return acc;
+}
+
+// Firing bitmap of a clause by walking its include mask (no literal list), on the
+// literal-major sample xt: lane j of each round of 64 finds the j-th included literal, and
+// the literals are AND-ed 8 per step (a short last step repeats one).
+__device__ __forceinline__ uint32_t firing_from_mask(const Geom& g, const uint32_t* m, const uint32_t* xt, uint32_t acc) {
+  const int lane = lane_id();
+  const int PW = (int)((g.P + 31) / 32);
+  const int jl = lane < PW ? lane : 0;
+  bool alive = true;
+  for (int64_t wb = 0; wb < g.W && alive; wb += kWave) {
+    const uint32_t mv = wb + lane < g.W ? m[wb + lane] : 0u;
+    const int pc = __popc(mv);
+    const int incl = wave_inclusive_scan(pc);
+    const int tot = lane_value(incl, kWave - 1);
+    const int nw = (int)(g.W - wb < kWave ? g.W - wb : kWave);
+    for (int jb = 0; jb < tot && alive; jb += kWave) {
+      const int j = jb + lane;
+      uint32_t mw = 0u;
+      int q = 0, ex = 0, before = 0;
+      for (int w = 0; w < nw; ++w) {
+        const int after = lane_value(incl, w);
+        if (before <= j && j < after) {
+          q = w;
+          ex = before;
+          mw = (uint32_t)lane_value((int)mv, w);
+        }
+        before = after;
+      }
+      int r = j - ex, pos = 0;
+      uint32_t v = mw;
+#pragma unroll
+      for (int width = 16; width > 0; width >>= 1) {
+        const int lowc = __popc(v & ((1u << width) - 1u));
+        if (r >= lowc) {
+          r -= lowc;
+          v >>= width;
+          pos += width;
+        }
+      }
+      const int lit = (int)(32 * (wb + q)) + pos;  // valid for lanes j < tot
+      const int cnt = tot - jb < kWave ? tot - jb : kWave;
+      for (int jj = 0; jj < cnt; jj += 8) {
+        uint32_t vv = 0xFFFFFFFFu;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int l = lane_value(lit, jj + u < cnt ? jj + u : jj);
+          vv &= xt[l * PW + jl];
+        }
+        acc &= vv;
+        if (((jj >> 3) & 1) && !__any(acc != 0u)) {
+          alive = false;
+          break;
+        }
+      }
+    }
+  }
+  return acc;
+}
+
+// Phase A for one clause of a model with several patches, on the literal-major sample xt
+// ([L][PW] words, PW = ceil(P/32) <= 64; bit b of word j of literal l: literal l set in
+// patch 32j + b).  The clause fires on the patches where every included literal is set, so
+// its firing bitmap is the AND of its included literals' bitsets (fast_eval,
+// kernel.cu:255-282), taken from the clause's literal list when it has one (nlist <= cap,
+// cap > 0) and from its include mask otherwise.  Then the reservoir choice of the firing
+// patch (select_active, kernel.cu:285-316).  An empty clause fires on every patch in
+// training.  Wave-uniform.
+template <bool INJECT>
+__device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, const uint32_t* m,
+                              const uint16_t* list, int nlist, int cap, const uint32_t* xt, bool dropped,
+                              int* ninc_out) {
+  const int lane = lane_id();
+  int ninc;
+  if (cap > 0 && nlist <= cap) {
+    ninc = nlist;
+  } else {
+    const bool exact_count = g.maxinc < g.L;
+    int cnt = 0;
+    uint32_t any = 0u;
+    for (int64_t w = lane; w < g.W; w += kWave) {
+      const uint32_t mw = m[w];
+      if (exact_count) cnt += __popc(mw);
+      any |= mw;
+    }
+    ninc = exact_count ? wave_sum_i32(cnt) : (__any(any != 0u) ? 1 : 0);
+  }
+  *ninc_out = ninc;
+  if (dropped) return -1;
+  uint32_t acc = all_patches_word(g);
+  if (ninc != 0)
+    acc = (cap > 0 && nlist <= cap) ? firing_from_list(g, list, nlist, xt, acc) : firing_from_mask(g, m, xt, acc);
+  return select_from_bitmap<INJECT>(a, g, inj, c, t, acc);
 }
 
 // Phase A for one clause (wave-uniform): returns the selected patch or -1 and the
@@ -597,7 +700,10 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   int* s_ninc = s_sel + a.cpw;                                 // [cpw]
   int* s_task_idx = s_ninc + a.cpw;                            // [cpw]
   int* s_task_sb = s_task_idx + a.cpw;                         // [cpw] (zero: no precomputed draws)
-  uint32_t* s_xt = (uint32_t*)(s_task_sb + a.cpw);             // [L][PW] when literal_major_lds(g)
+  const int cap = VANILLA ? 0 : g.list_cap;                    // literal list capacity
+  int* s_nlit = s_task_sb + a.cpw;                             // [cpw] include counts (cap > 0)
+  uint16_t* s_lits = (uint16_t*)(s_nlit + (cap > 0 ? 2 * ((a.cpw + 1) / 2) : 0));  // [cpw][cap] literal lists
+  uint32_t* s_xt = (uint32_t*)(s_lits + (int64_t)a.cpw * cap);  // [L][PW] when literal_major_lds(g)
   const int64_t cw = (int64_t)g.np * g.W;
   const int64_t xt_words = literal_major(g) ? g.L * ((g.P + 31) / 32) : 0;
   unsigned long long my_updates = 0ull;
@@ -608,6 +714,12 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   uint64_t prof_last = t_kernel;
   if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_abort = 0;
+  if (cap > 0)  // literal lists of the own clauses (visible after the first barrier below)
+    for (int idx = wave; idx < n_own; idx += (int)(blockDim.x / kWave)) {
+      const int n = build_literal_list(g, a.planes + (c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W,
+                                       s_lits + (int64_t)idx * cap, cap);
+      if (lane == 0) s_nlit[idx] = n;
+    }
 
   for (int i = 0; i < a.N; ++i) {
     const uint64_t t = a.step0 + (uint64_t)i;
@@ -640,7 +752,8 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       int ninc;
       const uint32_t* m = a.planes + (c * g.np + g.np - 1) * g.W;
       const int sel = (!VANILLA && literal_major(g))
-                          ? eval_select_lm<INJECT>(a, g, inj, c, t, m, xt, a.drop[c] == 1u, &ninc)
+                          ? eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * cap,
+                                                   cap > 0 ? s_nlit[idx] : 0, cap, xt, a.drop[c] == 1u, &ninc)
                           : eval_select<VANILLA, INJECT>(a, g, inj, c, t, m, xe, a.drop[c] == 1u, -1.0f, &ninc);
       if (lane == 0) {
         s_sel[idx] = sel;
@@ -680,19 +793,16 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       const FbOps ops = decide<INJECT, false>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob,
                                               a.weights + c * g.K, nullptr, nullptr);
       if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
-      if (lane == 0) ++my_updates;
-      if (g.W <= 32) {
-        if (lane == 0) {
-          const int tk = atomicAdd(&s_ntask, 1);
-          s_task_idx[tk] = idx;
-          s_task_sb[tk] = 0;
-          s_task_m[tk * 3 + 0] = ops.m1a;
-          s_task_m[tk * 3 + 1] = ops.m1b;
-          s_task_m[tk * 3 + 2] = ops.m2;
-        }
-      } else {
-        apply_ops<INJECT>(a, g, inj, c, t, s_sel[idx], ops, a.planes + c * cw, xe, nullptr);
+      if (lane == 0) {
+        ++my_updates;
+        const int tk = atomicAdd(&s_ntask, 1);
+        s_task_idx[tk] = idx;
+        s_task_sb[tk] = 0;
+        s_task_m[tk * 3 + 0] = ops.m1a;
+        s_task_m[tk * 3 + 1] = ops.m1b;
+        s_task_m[tk * 3 + 2] = ops.m2;
       }
+      if (g.W > 32) apply_ops<INJECT>(a, g, inj, c, t, s_sel[idx], ops, a.planes + c * cw, xe, nullptr);
     }
     if (g.W <= 32) {
       __syncthreads();
@@ -705,6 +815,15 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     }
     YTM_PROF_MARK(4);
     __syncthreads();
+    if (cap > 0) {  // the literal lists of the updated clauses (visible after the next barrier)
+      const int ntask = s_ntask;
+      for (int tk = wave; tk < ntask; tk += (int)(blockDim.x / kWave)) {
+        const int idx = s_task_idx[tk];
+        const int n = build_literal_list(g, a.planes + (c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W,
+                                         s_lits + (int64_t)idx * cap, cap);
+        if (lane == 0) s_nlit[idx] = n;
+      }
+    }
     YTM_PROF_MARK(5);
   }
   if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
@@ -772,7 +891,8 @@ template <bool INJECT>
 __device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int idx,
                                               const uint32_t* s_planes, const float* s_w, const int* s_drop,
                                               const uint32_t* s_x, const uint32_t* s_xt, const float* s_usel,
-                                              int* sel_out, int* ninc_out, int* s_pw, long long* part) {
+                                              const uint16_t* s_lits, const int* s_nlit, int* sel_out, int* ninc_out,
+                                              int* s_pw, long long* part) {
   const int lane = lane_id();
   const int64_t c = c_begin + idx;
   const uint64_t t = a.step0 + (uint64_t)j;
@@ -788,7 +908,8 @@ __device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g,
     sel = eval_select<true, INJECT, !INJECT>(a, g, inj, c, t, m, s_x + (j % 3) * g.W, dropped,
                                              INJECT ? -1.0f : s_usel[(j % 3) * a.cpw + idx], &ninc);
   else
-    sel = eval_select_lm<INJECT>(a, g, inj, c, t, m, s_xt + (int64_t)(j & 1) * g.L * ((g.P + 31) / 32), dropped, &ninc);
+    sel = eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * g.list_cap, g.list_cap > 0 ? s_nlit[idx] : 0,
+                                 g.list_cap, s_xt + (int64_t)(j & 1) * g.L * ((g.P + 31) / 32), dropped, &ninc);
   if (lane == 0) {
     sel_out[idx] = sel;
     ninc_out[idx] = ninc;
@@ -836,8 +957,11 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   const int R = a.rng_slots;
   const int cpw = a.cpw;
   const int64_t xtw = g.P > 1 ? g.L * ((g.P + 31) / 32) : 0;     // literal-major sample words
+  const int cap = g.P > 1 ? g.list_cap : 0;                       // literal list capacity
   unsigned long long* s_task_m = (unsigned long long*)dyn_lds;    // [cpw][3] feedback masks
-  uint32_t* s_xt = (uint32_t*)(s_task_m + 3 * cpw);               // [2][L][PW] (several patches)
+  uint16_t* s_lits = (uint16_t*)(s_task_m + 3 * cpw);             // [cpw][cap] literal lists
+  int* s_nlit = (int*)(s_lits + (int64_t)cpw * cap);              // [cpw] include counts
+  uint32_t* s_xt = (uint32_t*)(s_nlit + (cap > 0 ? 2 * ((cpw + 1) / 2) : 0));  // [2][L][PW]
   uint32_t* s_planes = s_xt + 2 * xtw;                            // [cpw][np][W]
   float* s_w = (float*)(s_planes + cpw * cw);                     // [cpw][K]
   uint32_t* s_x = (uint32_t*)(s_w + cpw * g.K);                   // [3][W]
@@ -884,10 +1008,17 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   }
   uint64_t spec_ticks = 0;  // profile: this wave's time in step 1 (waves >= 1)
   __syncthreads();
+  if (cap > 0) {
+    for (int idx = wave; idx < n_own; idx += nwv) {
+      const int n = build_literal_list(g, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W, s_lits + (int64_t)idx * cap, cap);
+      if (lane == 0) s_nlit[idx] = n;
+    }
+    __syncthreads();
+  }
   // Phase A of sample 0, every wave.
   if (a.N > 0)
     for (int idx = wave; idx < n_own; idx += nwv)
-      resident_eval<INJECT>(a, g, 0, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel, s_ninc, s_pw,
+      resident_eval<INJECT>(a, g, 0, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, s_sel, s_ninc, s_pw,
                             s_part[0]);
   __syncthreads();
   prof_last = __builtin_amdgcn_s_memrealtime();
@@ -912,7 +1043,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       const uint64_t spec_t0 = a.profile ? __builtin_amdgcn_s_memrealtime() : 0;
       if (more)
         for (int idx = wave - 1; idx < n_own; idx += nwv - 1)
-          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel + b2n * cpw,
+          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, s_sel + b2n * cpw,
                                 s_ninc + b2n * cpw, s_pw, s_part[b2n]);
       if (i + 2 < a.N) {
         const int b3nn = (i + 2) % 3;
@@ -1002,10 +1133,17 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       for (int tk0 = wave * per; tk0 < ntask; tk0 += nwv * per) {
         apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb,
                             s_sel + b2 * cpw, s_planes, xe, INJECT ? nullptr : s_rng, R);
+        if (cap > 0)
+          for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk) {
+            const int idx = s_task_idx[tk];
+            const int n = build_literal_list(g, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W,
+                                             s_lits + (int64_t)idx * cap, cap);
+            if (lane == 0) s_nlit[idx] = n;
+          }
         if (more)
           for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk)
             resident_eval<INJECT>(a, g, i + 1, c_begin, s_task_idx[tk], s_planes, s_w, s_drop, s_x, s_xt, s_usel,
-                                  s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+                                  s_lits, s_nlit, s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
       }
     } else {
       for (int tk = wave; tk < ntask; tk += nwv) {  // tasks round-robin over the waves
@@ -1015,8 +1153,13 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         const bool have = !INJECT && sb + __popcll(ops.m1a | ops.m1b) <= R;
         apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[b2 * cpw + idx], ops, s_planes + idx * cw, xe,
                           have ? s_rng + (int64_t)sb * g.W * (kPreGroups * 4) : nullptr);
+        if (cap > 0) {
+          const int n = build_literal_list(g, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W,
+                                           s_lits + (int64_t)idx * cap, cap);
+          if (lane == 0) s_nlit[idx] = n;
+        }
         if (more)
-          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_sel + b2n * cpw,
+          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, s_sel + b2n * cpw,
                                 s_ninc + b2n * cpw, s_pw, s_part[b2n]);
       }
     }

@@ -6,6 +6,7 @@
 #include <stdint.h>
 #else
 // hipRTC's built-in preamble declares the fixed-width integer types in __hip_internal.
+using __hip_internal::uint16_t;
 using __hip_internal::int32_t;
 using __hip_internal::int64_t;
 using __hip_internal::uint32_t;
@@ -52,7 +53,8 @@ constexpr int kMaxPlanesHost = 16;  // must equal kMaxPlanes of ytm_device.h
   X(int, threads)          /* training launch: threads per workgroup (0 outside training) */        \
   X(int, grid)             /* training launch: persistent workgroups (0 outside training) */         \
   X(int, group_size)       /* training launch: workgroups per class-sum group */                     \
-  X(int, groups)           /* training launch: class-sum groups, ceil(grid / group_size) */
+  X(int, groups)           /* training launch: class-sum groups, ceil(grid / group_size) */          \
+  X(int, list_cap)         /* training launch: literal-list capacity per clause (0: none) */
 
 struct Geom {
 #define YTM_GEOM_DECL(type, name) type name;
