@@ -548,13 +548,18 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (N == 0) return YTM_OK;
   long long* acc = nullptr;
   float* dout = nullptr;
+  void* lists = nullptr;  // several patches: the clauses' literal lists
+  const size_t lists_bytes = ds->d_XT ? ytm::score_lists_bytes(g) : 0;
   HIP_TRY(hipMalloc(&acc, (size_t)(N * g.K) * 8));
   hipError_t e = hipMalloc(&dout, (size_t)(N * g.K) * 4);
+  if (e == hipSuccess && lists_bytes) e = hipMalloc(&lists, lists_bytes);
   int rc = YTM_OK;
   if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
   if (e == hipSuccess) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
   if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
-  if (e == hipSuccess) e = ytm::launch_score(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->stream);
+  if (e == hipSuccess)
+    e = lists ? ytm::launch_score_lm(m->d_planes, m->d_w, ds->d_XT, N, g, lists, acc, m->stream)
+              : ytm::launch_score(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->stream);
   if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
   if (e == hipSuccess) e = ytm::launch_score_finish(acc, m->d_bias, N, g, dout, m->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(class_sums, dout, (size_t)(N * g.K) * 4, hipMemcpyDeviceToHost, m->stream);
@@ -565,6 +570,7 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   m->stats.last_score_kernel_ms = ms;
   if (acc) (void)hipFree(acc);
   if (dout) (void)hipFree(dout);
+  if (lists) (void)hipFree(lists);
   return rc;
 }
 

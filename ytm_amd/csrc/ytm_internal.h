@@ -20,6 +20,11 @@ hipError_t launch_ninc(const uint32_t* planes, int32_t* ninc, const Geom& g, hip
 hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s);
 hipError_t launch_score(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
                         int64_t N, const Geom& g, long long* acc, hipStream_t s);
+// Scoring of several-patch models on literal-major samples; scratch holds score_lists_bytes(g)
+// (0: not available for this geometry).
+size_t score_lists_bytes(const Geom& g);
+hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_t* XT, int64_t N, const Geom& g,
+                           void* scratch, long long* acc, hipStream_t s);
 hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t N, const Geom& g,
                                float* out, hipStream_t s);
 hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const uint32_t* X, int64_t N,

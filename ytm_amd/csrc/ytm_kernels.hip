@@ -317,6 +317,88 @@ __global__ __launch_bounds__(256) void score_tile_kernel(const uint32_t* __restr
   }
 }
 
+// Several patches: the included literals of every clause as a list (build_literal_list),
+// [C][cap] with the include counts [C]; one wave per clause.
+__global__ __launch_bounds__(256) void build_lists_kernel(const uint32_t* __restrict__ planes, Geom g, int cap,
+                                                          uint16_t* __restrict__ lists, int32_t* __restrict__ nlit) {
+  const int lane = lane_id();
+  const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / kWave;
+  const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
+  for (int64_t c = wave; c < g.C; c += nwaves) {
+    const int n = build_literal_list(g, planes + (c * g.np + g.np - 1) * g.W, lists + c * cap, cap);
+    if (lane == 0) nlit[c] = n;
+  }
+}
+
+// Firing bitmap from a literal list held in registers: lane q has entries [8q, 8q + 8) in
+// lv (the list padded to a multiple of 8), read 8 at a time with readlane.
+__device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 lv, int n, const uint32_t* xt,
+                                                          uint32_t acc) {
+  const int lane = lane_id();
+  const int PW = (int)((g.P + 31) / 32);
+  const int jl = lane < PW ? lane : 0;
+  for (int j = 0; j < n; j += 8) {
+    const int src = j >> 3;
+    const uint32_t q[4] = {(uint32_t)lane_value((int)lv.x, src), (uint32_t)lane_value((int)lv.y, src),
+                           (uint32_t)lane_value((int)lv.z, src), (uint32_t)lane_value((int)lv.w, src)};
+    uint32_t v = 0xFFFFFFFFu;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v &= xt[(q[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)jl];
+      v &= xt[(q[u] >> 16) * (uint32_t)PW + (uint32_t)jl];
+    }
+    acc &= v;
+    if ((j & 8) && !__any(acc != 0u)) break;
+  }
+  return acc;
+}
+
+// Several patches (literal-major samples): one block per (sample, chunk of clauses); the
+// sample's literal-major copy is staged in LDS and each wave decides, clause by clause,
+// whether any patch fires (the AND of the included literals' bitsets, from the clause's
+// literal list when it has one) -- calc_class_sums_infer_batch, kernel.cu:319-343 (empty
+// clauses do not vote).  Lanes < K sum the weights of the firing clauses exactly.
+constexpr int64_t kScoreLmChunk = 4096;
+constexpr int kScoreListCap = 256;
+
+__global__ __launch_bounds__(256) void score_lm_kernel(const uint32_t* __restrict__ planes,
+                                                       const uint16_t* __restrict__ lists,
+                                                       const int32_t* __restrict__ nlit, const float* __restrict__ w,
+                                                       const uint32_t* __restrict__ XT, int64_t N, Geom g,
+                                                       long long* __restrict__ acc) {
+  extern __shared__ uint32_t s_xts[];  // [L][PW]
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave, nwv = blockDim.x / kWave;
+  const int64_t xtw = g.L * ((g.P + 31) / 32);
+  const int64_t nch = (g.C + kScoreLmChunk - 1) / kScoreLmChunk;
+  for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
+    const int64_t e = blk / nch, ch = blk % nch;
+    const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
+    __syncthreads();  // the previous sample is no longer read
+    const uint32_t* src = XT + e * xtw;
+    if ((xtw & 1) == 0) {
+      for (int64_t j = threadIdx.x; j < xtw / 2; j += blockDim.x) ((uint2*)s_xts)[j] = ((const uint2*)src)[j];
+    } else {
+      for (int64_t j = threadIdx.x; j < xtw; j += blockDim.x) s_xts[j] = src[j];
+    }
+    __syncthreads();
+    long long sum = 0;
+    for (int64_t c = c0 + wave; c < c1; c += nwv) {
+      const int n = nlit[c];
+      if (n == 0) continue;  // empty clauses do not vote
+      uint32_t fire = all_patches_word(g);
+      if (n <= kScoreListCap) {
+        const uint4 lv = 8 * lane < n ? *(const uint4*)(lists + c * kScoreListCap + 8 * lane) : uint4{0u, 0u, 0u, 0u};
+        fire = firing_from_list_regs(g, lv, n, s_xts, fire);
+      } else {
+        fire = firing_from_mask(g, planes + (c * g.np + g.np - 1) * g.W, s_xts, fire);
+      }
+      if (__any(fire != 0u) && lane < g.K) sum += (long long)w[c * g.K + lane];
+    }
+    if (lane < g.K && sum != 0) atomicAdd((unsigned long long*)&acc[e * g.K + lane], (unsigned long long)sum);
+  }
+}
+
 __global__ __launch_bounds__(256) void score_finish_kernel(const long long* __restrict__ acc,
                                                            const float* __restrict__ bias, int64_t N,
                                                            Geom g, float* __restrict__ out) {
@@ -416,6 +498,22 @@ hipError_t launch_ninc(const uint32_t* planes, int32_t* ninc, const Geom& g, hip
 
 hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s) {
   fill_u64_kernel<<<grid_for(n, 256), 256, 0, s>>>(p, n);
+  return hipGetLastError();
+}
+
+size_t score_lists_bytes(const Geom& g) {
+  if (!literal_major(g) || g.L > 65535 || (size_t)(g.L * ((g.P + 31) / 32)) * 4 > 120 * 1024) return 0;
+  return (size_t)g.C * kScoreListCap * 2 + (size_t)g.C * 4;
+}
+
+hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_t* XT, int64_t N, const Geom& g,
+                           void* scratch, long long* acc, hipStream_t s) {
+  uint16_t* lists = (uint16_t*)scratch;
+  int32_t* nlit = (int32_t*)(lists + g.C * kScoreListCap);
+  build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
+  const int64_t blocks = N * ((g.C + kScoreLmChunk - 1) / kScoreLmChunk);
+  const int grid = blocks < 65536 ? (int)blocks : 65536;
+  score_lm_kernel<<<grid, 256, (size_t)(g.L * ((g.P + 31) / 32)) * 4, s>>>(planes, lists, nlit, w, XT, N, g, acc);
   return hipGetLastError();
 }
 
