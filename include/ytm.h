@@ -131,8 +131,14 @@ int ytm_score_dataset(ytm_model *m, const ytm_dataset *ds, float *class_sums);
 int ytm_score(ytm_model *m, const uint32_t *encX, int64_t N, float *class_sums);
 
 /* transform / transform_patchwise (src/cutm/base.py:465-542; kernel.cu:346-394).
- * patchwise = 0: out uint32 (N, clauses); patchwise = 1: out uint32 (N, clauses, P). */
-int ytm_transform(ytm_model *m, const uint32_t *encX, int64_t N, int patchwise, uint32_t *out);
+ * mode 0: out uint32 (N, clauses), 1 where some patch fires;
+ * mode 1: out uint32 (N, clauses, P), one value per patch;
+ * mode 2: out uint32 (N, clauses, ceil(P/32)), the mode-1 values bit-packed: bit b of word j
+ *         is patch 32j + b, bits beyond P are 0 (an option the reference does not have, for
+ *         outputs of C*P*N values that would not fit as one uint32 each).
+ * Empty clauses output 1.  Samples are processed in chunks, so device memory stays bounded
+ * whatever N is. */
+int ytm_transform(ytm_model *m, const uint32_t *encX, int64_t N, int mode, uint32_t *out);
 
 /* State accessors (src/cutm/base.py:423-461, 561-593), flat C-order.
  * ta_state: uint32 (clauses, L); weights: float (clauses, classes);

@@ -212,8 +212,80 @@ def test_score_transform(cfg, n_train, n_test, clauses):
     np.testing.assert_array_equal(preds, np.argmax(ref_cs, axis=1))
     np.testing.assert_array_equal(tm.transform(encXt, is_X_encoded=True), ref.transform(encXt))
     n_pw = min(n_test, 12)
-    np.testing.assert_array_equal(tm.transform_patchwise(encXt[:n_pw], is_X_encoded=True),
-                                  ref.transform(encXt[:n_pw], patchwise=True))
+    ref_pw = ref.transform(encXt[:n_pw], patchwise=True)
+    np.testing.assert_array_equal(tm.transform_patchwise(encXt[:n_pw], is_X_encoded=True), ref_pw)
+    assert_packed_equal(tm.transform_patchwise(encXt[:n_pw], is_X_encoded=True, packed=True), ref_pw)
+
+
+def assert_packed_equal(packed, ref_pw):
+    """packed: uint32 (N, C, ceil(P/32)), bit b of word j = patch 32j + b, zero beyond P."""
+    P = ref_pw.shape[2]
+    assert packed.dtype == np.uint32 and packed.shape == ref_pw.shape[:2] + ((P + 31) // 32,)
+    bits = np.unpackbits(np.ascontiguousarray(packed).view(np.uint8), axis=-1, bitorder="little")
+    np.testing.assert_array_equal(bits[..., :P], ref_pw)
+    assert not bits[..., P:].any()
+
+
+def random_state(tm, ref, rng, include_p):
+    """Random TA states (each literal included with probability include_p[c] per clause)
+    and random integer weights, loaded into both models."""
+    C, L, K = tm.number_of_clauses, tm.number_of_literals, ref.w.shape[1]
+    half = tm.number_of_ta_states // 2
+    inc = rng.random((C, L)) < np.asarray(include_p)[:, None]
+    ta = np.where(inc, rng.integers(half + 1, 2 * half + 1, (C, L)), rng.integers(0, half + 1, (C, L)))
+    ta = ta.astype(np.uint32)
+    w = rng.integers(-50, 51, (C, K)).astype(np.float32)
+    pw = np.zeros((C, tm.number_of_patches), dtype=np.int32)
+    tm.load_state_dict({"state": {"ta_state": ta, "clause_weights": w, "patch_weights": pw,
+                                  "min_y": None, "max_y": None}})
+    ref.ta[...] = ta.reshape(ref.ta.shape)
+    ref.w[...] = w.reshape(ref.w.shape)
+
+
+@pytest.mark.parametrize("dim,patch_dim,classes,clauses", [
+    ((100, 1, 1), None, 3, 300),     # one patch, 7 words
+    ((30, 1, 1), None, 20, 200),     # one patch, more classes than the tiled scorer holds
+    ((1500, 1, 1), None, 2, 150),    # one patch, 94 words
+    ((12, 12, 2), (4, 4), 4, 300),   # several patches, literal lists
+    ((16, 16, 16), (3, 3), 3, 120),  # several patches, 340 literals: some clauses beyond the list capacity
+])
+def test_inference_random_state(dim, patch_dim, classes, clauses):
+    """Class sums and clause outputs on random states: every inference kernel variant
+    (tiles, lists, the include-mask fallback) against the oracle."""
+    kw = dict(number_of_clauses_per_class=clauses, T=50, s=5.0, dim=dim, n_classes=classes, seed=7)
+    if patch_dim is not None:
+        kw["patch_dim"] = patch_dim
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(clauses, 50, 5.0, dim, classes, **({"patch_dim": patch_dim} if patch_dim else {}), seed=7)
+    rng = np.random.default_rng(11)
+    L = tm.number_of_literals
+    # mostly narrow clauses (these fire), some empty ones, some with over 256 literals
+    include_p = np.where(rng.random(tm.number_of_clauses) < 0.1, 0.0, 3.0 / L)
+    include_p[rng.random(tm.number_of_clauses) < 0.05] = min(1.0, 300.0 / L)
+    random_state(tm, ref, rng, include_p)
+    X = (rng.random((70,) + tuple(dim)) < 0.5).astype(np.uint32).reshape(70, -1)
+    encX = tm.encode(X)
+    np.testing.assert_array_equal(encX, ref.encode(X))
+    np.testing.assert_array_equal(tm.score(encX, is_X_encoded=True), ref.score(encX))
+    np.testing.assert_array_equal(tm.transform(encX, is_X_encoded=True), ref.transform(encX))
+    ref_pw = ref.transform(encX[:9], patchwise=True)
+    np.testing.assert_array_equal(tm.transform_patchwise(encX[:9], is_X_encoded=True), ref_pw)
+    assert_packed_equal(tm.transform_patchwise(encX[:9], is_X_encoded=True, packed=True), ref_pw)
+
+
+def test_transform_in_chunks(monkeypatch):
+    """Samples go through transform in chunks (forced small here): ragged last chunk, the
+    literal lists built once and reused."""
+    tm, ref, X, y, Xt, yt = pair(3, 30, 23, clauses=60)
+    encX = tm.encode(X)
+    tm.fit(encX, y, is_X_encoded=True)
+    ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+    encXt = tm.encode(Xt)
+    monkeypatch.setenv("YTM_TRANSFORM_CHUNK", "5")
+    np.testing.assert_array_equal(tm.transform(encXt, is_X_encoded=True), ref.transform(encXt))
+    ref_pw = ref.transform(encXt, patchwise=True)
+    np.testing.assert_array_equal(tm.transform_patchwise(encXt, is_X_encoded=True), ref_pw)
+    assert_packed_equal(tm.transform_patchwise(encXt, is_X_encoded=True, packed=True), ref_pw)
 
 
 def test_score_edge_cases():

@@ -341,18 +341,31 @@ class BaseTM:
         check(lib.ytm_transform(self._handle, ptr(encoded_X), N, 0, ptr(out)))
         return out
 
-    def transform_patchwise(self, X, is_X_encoded: bool = False, block_size: int | None = None) -> np.ndarray:
+    def transform_patchwise(self, X, is_X_encoded: bool = False, block_size: int | None = None,
+                            packed: bool = False) -> np.ndarray:
+        """Per-patch clause outputs (src/cutm/base.py:510-542): uint32 (N, clauses, patches).
+
+        ``packed=True`` (not in the reference) returns the same values bit-packed, uint32
+        (N, clauses, ceil(patches / 32)) with bit b of word j = patch 32j + b and zero bits
+        beyond the last patch -- 1/32 of the memory.  ``np.unpackbits(out.view(np.uint8),
+        axis=-1, bitorder="little")[..., :patches]`` recovers the unpacked array on a
+        little-endian host.
+        """
         encoded_X = X if is_X_encoded else self.encode(X)
         N = encoded_X.shape[0]
-        max_safe_N = np.iinfo(np.uint32).max // (self.number_of_clauses * self.number_of_patches)
+        P = self.number_of_patches
+        per_clause = (P + 31) // 32 if packed else P
+        max_safe_N = np.iinfo(np.uint32).max // (self.number_of_clauses * per_clause)
         if N > max_safe_N:
             raise OverflowError(
                 f"X has too many samples ({N}). Maximum of {max_safe_N} samples can be processed with current "
-                "number_of_clauses * number_of_patches. Call this method multiple times with smaller batches of X."
+                + ("number_of_clauses * ceil(number_of_patches / 32)" if packed
+                   else "number_of_clauses * number_of_patches")
+                + ". Call this method multiple times with smaller batches of X."
             )
         encoded_X = self._check_encoded(encoded_X)
-        out = np.empty((N, self.number_of_clauses, self.number_of_patches), dtype=np.uint32)
-        check(lib.ytm_transform(self._handle, ptr(encoded_X), N, 1, ptr(out)))
+        out = np.empty((N, self.number_of_clauses, per_clause), dtype=np.uint32)
+        check(lib.ytm_transform(self._handle, ptr(encoded_X), N, 2 if packed else 1, ptr(out)))
         return out
 
     # ------------------------------------------------------------------ serialisation

@@ -584,22 +584,46 @@ int ytm_score(ytm_model* m, const uint32_t* encX, int64_t N, float* class_sums) 
   return rc;
 }
 
-int ytm_transform(ytm_model* m, const uint32_t* encX, int64_t N, int patchwise, uint32_t* out) {
-  if (!m || N < 0 || (N > 0 && (!encX || !out))) return fail(YTM_EINVAL, "bad transform arguments");
+int ytm_transform(ytm_model* m, const uint32_t* encX, int64_t N, int mode, uint32_t* out) {
+  if (!m || N < 0 || mode < 0 || mode > 2 || (N > 0 && (!encX || !out)))
+    return fail(YTM_EINVAL, "bad transform arguments");
   if (N == 0) return YTM_OK;
   const Geom& g = m->g;
-  const size_t out_n = (size_t)(N * g.C * (patchwise ? g.P : 1));
-  uint32_t *dX = nullptr, *dO = nullptr;
-  int rc = upload((void**)&dX, encX, (size_t)(N * g.P * g.W) * 4, m->stream);
-  if (rc) return rc;
-  hipError_t e = hipMalloc(&dO, out_n * 4);
+  const int64_t PW = (g.P + 31) / 32;
+  const int64_t per_out = g.C * (mode == 0 ? 1 : (mode == 1 ? g.P : PW));  // uint32 per sample
+  const size_t lists_bytes = ytm::score_lists_bytes(g);
+  const bool lm = lists_bytes > 0;
+  const int64_t per_in = g.P * g.W + (lm ? g.L * PW : 0);
+  // Device buffers per pass stay within ~1 GiB; samples go through in chunks.
+  int64_t chunk = ((int64_t)1 << 30) / ((per_out + per_in) * 4);
+  if (const char* v = std::getenv("YTM_TRANSFORM_CHUNK")) chunk = std::atoll(v);  // samples per pass
+  chunk = chunk < 1 ? 1 : (chunk > N ? N : chunk);
+  uint32_t *dX = nullptr, *dXT = nullptr, *dO = nullptr;
+  void* dL = nullptr;
+  hipError_t e = hipMalloc(&dX, (size_t)(chunk * g.P * g.W) * 4);
+  if (e == hipSuccess) e = hipMalloc(&dO, (size_t)(chunk * per_out) * 4);
+  if (e == hipSuccess && lm) e = hipMalloc(&dXT, (size_t)(chunk * g.L * PW) * 4);
+  if (e == hipSuccess && lm) e = hipMalloc(&dL, lists_bytes);
   if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
-  if (e == hipSuccess) e = ytm::launch_transform(m->d_planes, m->d_ninc, dX, N, g, patchwise, dO, m->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(out, dO, out_n * 4, hipMemcpyDeviceToHost, m->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
-  if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("transform failed: ") + hipGetErrorString(e));
-  (void)hipFree(dX);
+  for (int64_t first = 0; e == hipSuccess && first < N; first += chunk) {
+    const int64_t n = N - first < chunk ? N - first : chunk;
+    e = hipMemcpyAsync(dX, encX + first * g.P * g.W, (size_t)(n * g.P * g.W) * 4, hipMemcpyHostToDevice,
+                       m->stream);
+    if (e == hipSuccess && lm) {
+      e = ytm::launch_transpose(dX, n, dXT, g, m->stream);
+      if (e == hipSuccess) e = ytm::launch_transform_lm(m->d_planes, dXT, n, g, mode, dL, first > 0, dO, m->stream);
+    } else if (e == hipSuccess) {
+      e = ytm::launch_transform(m->d_planes, m->d_ninc, dX, n, g, mode, dO, m->stream);
+    }
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(out + first * per_out, dO, (size_t)(n * per_out) * 4, hipMemcpyDeviceToHost, m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  }
+  const int rc = e == hipSuccess ? YTM_OK : fail(YTM_EHIP, std::string("transform failed: ") + hipGetErrorString(e));
+  if (dX) (void)hipFree(dX);
   if (dO) (void)hipFree(dO);
+  if (dXT) (void)hipFree(dXT);
+  if (dL) (void)hipFree(dL);
   return rc;
 }
 

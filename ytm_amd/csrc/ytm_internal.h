@@ -27,8 +27,14 @@ hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_
                            void* scratch, long long* acc, hipStream_t s);
 hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t N, const Geom& g,
                                float* out, hipStream_t s);
+// Clause outputs; mode 0: any patch (N, C); 1: per patch (N, C, P); 2: per patch, bit-packed
+// (N, C, ceil(P/32)).
 hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const uint32_t* X, int64_t N,
-                            const Geom& g, int patchwise, uint32_t* out, hipStream_t s);
+                            const Geom& g, int mode, uint32_t* out, hipStream_t s);
+// The same on literal-major samples; scratch holds score_lists_bytes(g), its literal lists
+// built first unless lists_ready.
+hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64_t N, const Geom& g, int mode,
+                               void* scratch, bool lists_ready, uint32_t* out, hipStream_t s);
 
 // Training kernel variants: clause state resident in LDS (one patch), or kept in global
 // memory (one patch / several patches).

@@ -407,8 +407,157 @@ __global__ __launch_bounds__(256) void score_finish_kernel(const long long* __re
     out[i] = (float)(acc[i] + (long long)bias[i % g.K]);
 }
 
-// transform (kernel.cu:346-368) and transform_patchwise (kernel.cu:370-394).
-template <bool VANILLA, bool PATCHWISE>
+// One patch, lanes = samples: a block stages kTileC clauses' include masks (rows padded to
+// a multiple of 4 words, zero beyond W) in LDS; each of its four waves holds the
+// complements of its own 64 samples' words in VGPRs and tests every staged clause with one
+// AND-OR per word against a broadcast LDS row.  MODE 0 adds the firing clauses' weights into
+// per-lane class sums (calc_class_sums_infer_batch, kernel.cu:319-343: empty clauses do not
+// vote); MODE 1 writes clause outputs (transform, kernel.cu:346-368, and transform_patchwise
+// with its single patch: empty clauses output 1) through per-clause ballots in LDS, so that
+// each output row is written coalesced.  MAXQ bounds W by 4*MAXQ words.
+constexpr int kTileC = 128;
+constexpr int kTileMaxK = 16;
+
+template <int MAXQ, int MODE>
+__global__ __launch_bounds__(256) void tile_kernel(const uint32_t* __restrict__ planes,
+                                                   const int32_t* __restrict__ ninc, const float* __restrict__ w,
+                                                   const uint32_t* __restrict__ X, int64_t N, Geom g,
+                                                   long long* __restrict__ acc, uint32_t* __restrict__ out) {
+  __shared__ uint4 s_m[kTileC * MAXQ];
+  __shared__ long long s_w[MODE == 0 ? kTileC * kTileMaxK : 1];
+  __shared__ int s_live[kTileC];
+  __shared__ unsigned long long s_bal[MODE == 1 ? 4 * kTileC : 1];
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int Wq = (int)((g.W + 3) / 4);
+  const int64_t nsg = (N + 255) / 256;
+  const int64_t nch = (g.C + kTileC - 1) / kTileC;
+  for (int64_t blk = blockIdx.x; blk < nsg * nch; blk += gridDim.x) {
+    const int64_t e0 = (blk / nch) * 256 + wave * kWave, c0 = (blk % nch) * kTileC;
+    const int nc = (int)(c0 + kTileC < g.C ? kTileC : g.C - c0);
+    __syncthreads();  // the previous chunk is no longer read
+    for (int j = threadIdx.x; j < nc * 4 * MAXQ; j += blockDim.x) {
+      const int cl = j / (4 * MAXQ), ww = j % (4 * MAXQ);
+      ((uint32_t*)s_m)[j] = ww < g.W ? planes[((c0 + cl) * g.np + g.np - 1) * g.W + ww] : 0u;
+    }
+    for (int j = threadIdx.x; j < nc; j += blockDim.x) s_live[j] = ninc[c0 + j] != 0;
+    if (MODE == 0)
+      for (int j = threadIdx.x; j < nc * (int)g.K; j += blockDim.x) s_w[j] = (long long)w[c0 * g.K + j];
+    const int64_t e = e0 + lane;
+    uint32_t nx[4 * MAXQ];
+#pragma unroll
+    for (int ww = 0; ww < 4 * MAXQ; ++ww) nx[ww] = (ww < g.W && e < N) ? ~X[e * g.W + ww] : 0u;
+    long long sum[MODE == 0 ? kTileMaxK : 1];
+#pragma unroll
+    for (int k = 0; k < (MODE == 0 ? kTileMaxK : 1); ++k) sum[k] = 0;
+    __syncthreads();
+    for (int cl = 0; cl < nc; ++cl) {
+      const uint4* row = s_m + cl * MAXQ;
+      // Groups of up to 16 words: the group's LDS reads are issued together, and the wave
+      // stops once none of its samples can satisfy the clause.
+      uint32_t bad = 0u;
+#pragma unroll
+      for (int q0 = 0; q0 < MAXQ; q0 += 4) {
+        if (q0 < Wq && (q0 == 0 || __any(bad == 0u))) {
+          uint4 mv[MAXQ < 4 ? MAXQ : 4];
+#pragma unroll
+          for (int u = 0; u < (MAXQ < 4 ? MAXQ : 4); ++u) mv[u] = row[q0 + u];
+#pragma unroll
+          for (int u = 0; u < (MAXQ < 4 ? MAXQ : 4); ++u) {
+            const int b = 4 * (q0 + u);
+            bad |= (mv[u].x & nx[b]) | (mv[u].y & nx[b + 1]) | (mv[u].z & nx[b + 2]) | (mv[u].w & nx[b + 3]);
+          }
+        }
+      }
+      const bool live = s_live[cl] != 0;
+      if (MODE == 0) {
+        const bool fire = live && bad == 0u;
+        if (__any(fire)) {
+#pragma unroll
+          for (int k = 0; k < kTileMaxK; ++k)
+            if (k < g.K) sum[k] += fire ? s_w[cl * g.K + k] : 0ll;
+        }
+      } else {
+        const unsigned long long bits = __ballot(!live || bad == 0u);
+        if (lane == 0) s_bal[wave * kTileC + cl] = bits;
+      }
+    }
+    if (MODE == 0) {
+      if (e < N) {
+#pragma unroll
+        for (int k = 0; k < kTileMaxK; ++k)
+          if (k < g.K && sum[k] != 0) atomicAdd((unsigned long long*)&acc[e * g.K + k], (unsigned long long)sum[k]);
+      }
+    } else {
+      __syncthreads();  // the ballots are complete
+      const int rows = (int)(N - e0 < kWave ? N - e0 : kWave);
+      for (int r = 0; r < rows; ++r)
+        for (int cl = lane; cl < nc; cl += kWave)
+          out[(e0 + r) * g.C + c0 + cl] = (uint32_t)(s_bal[wave * kTileC + cl] >> r) & 1u;
+    }
+  }
+}
+
+// Several patches, literal-major samples: clause outputs (transform / transform_patchwise,
+// kernel.cu:346-394; an empty clause outputs 1 for every patch).  One block per (sample,
+// chunk of clauses) with the sample's literal-major copy in LDS, one wave per clause: the
+// firing bitmap over all patches is the AND of the included literals' bitsets (from the
+// clause's literal list when it has one).  MODE 0: out[e][c] = some patch fires;
+// MODE 1: out[e][c][p]; MODE 2: out[e][c][j] with bit b = patch 32j + b (0 beyond P).
+template <int MODE>
+__global__ __launch_bounds__(256) void transform_lm_kernel(const uint32_t* __restrict__ planes,
+                                                           const uint16_t* __restrict__ lists,
+                                                           const int32_t* __restrict__ nlit,
+                                                           const uint32_t* __restrict__ XT, int64_t N, Geom g,
+                                                           uint32_t* __restrict__ out) {
+  extern __shared__ uint32_t s_xts[];  // [L][PW]
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave, nwv = blockDim.x / kWave;
+  const int PW = (int)((g.P + 31) / 32);
+  const int64_t xtw = g.L * PW;
+  const int64_t nch = (g.C + kScoreLmChunk - 1) / kScoreLmChunk;
+  for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
+    const int64_t e = blk / nch, ch = blk % nch;
+    const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
+    __syncthreads();  // the previous sample is no longer read
+    const uint32_t* src = XT + e * xtw;
+    for (int64_t j = threadIdx.x; j < xtw; j += blockDim.x) s_xts[j] = src[j];
+    __syncthreads();
+    for (int64_t c = c0 + wave; c < c1; c += nwv) {
+      const int n = nlit[c];
+      uint32_t fire = all_patches_word(g);
+      if (n > 0) {
+        if (n <= kScoreListCap) {
+          const uint4 lv =
+              8 * lane < n ? *(const uint4*)(lists + c * kScoreListCap + 8 * lane) : uint4{0u, 0u, 0u, 0u};
+          fire = firing_from_list_regs(g, lv, n, s_xts, fire);
+        } else {
+          fire = firing_from_mask(g, planes + (c * g.np + g.np - 1) * g.W, s_xts, fire);
+        }
+      }
+      const int64_t ec = e * g.C + c;
+      if (MODE == 0) {
+        const bool any = __any(fire != 0u);
+        if (lane == 0) out[ec] = any ? 1u : 0u;
+      } else if (MODE == 2) {
+        if (lane < PW) out[ec * PW + lane] = fire;
+      } else {
+        for (int base = 0; base < (int)g.P; base += kWave) {
+          const int j = base >> 5;
+          const uint32_t lo = (uint32_t)lane_value((int)fire, j);
+          const uint32_t hi = j + 1 < PW ? (uint32_t)lane_value((int)fire, j + 1) : 0u;
+          const uint32_t bit = lane < 32 ? (lo >> lane) & 1u : (hi >> (lane - 32)) & 1u;
+          if (base + lane < (int)g.P) out[ec * g.P + base + lane] = bit;
+        }
+      }
+    }
+  }
+}
+
+// transform (kernel.cu:346-368) and transform_patchwise (kernel.cu:370-394) on the
+// reference's sample layout, one wave per (sample, clause).  MODE 0: any patch; 1: per
+// patch; 2: per patch, bit-packed as in transform_lm_kernel.
+template <bool VANILLA, int MODE>
 __global__ __launch_bounds__(256) void transform_kernel(const uint32_t* __restrict__ planes,
                                                         const int32_t* __restrict__ ninc,
                                                         const uint32_t* __restrict__ X, int64_t N, Geom g,
@@ -416,19 +565,21 @@ __global__ __launch_bounds__(256) void transform_kernel(const uint32_t* __restri
   const int lane = lane_id();
   const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / kWave;
   const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
+  const int64_t PW = (g.P + 31) / 32;
   for (int64_t ec = wave; ec < N * g.C; ec += nwaves) {
     const int64_t e = ec / g.C, c = ec % g.C;
     const uint32_t* m = planes + (c * g.np + g.np - 1) * g.W;
     const uint32_t* xe = X + e * g.P * g.W;
     const bool empty = ninc[c] == 0;
-    if (!PATCHWISE) {
+    if (MODE == 0) {
       const bool v = empty ? true : clause_fires_any<VANILLA>(m, xe, g);
       if (lane == 0) out[ec] = v ? 1u : 0u;
     } else {
       for (int64_t base = 0; base < g.P; base += kWave) {
         const int64_t p = base + lane;
+        uint32_t v = 0u;
         if (p < g.P) {
-          uint32_t v = 1u;
+          v = 1u;
           if (!empty) {
             const uint32_t* xp = xe + p * g.W;
             for (int64_t w = 0; w < g.W; ++w)
@@ -437,7 +588,12 @@ __global__ __launch_bounds__(256) void transform_kernel(const uint32_t* __restri
                 break;
               }
           }
-          out[ec * g.P + p] = v;
+          if (MODE == 1) out[ec * g.P + p] = v;
+        }
+        if (MODE == 2) {
+          const unsigned long long bits = __ballot(v != 0u);
+          const int64_t j = base / 32 + lane;
+          if (lane < 2 && j < PW) out[ec * PW + j] = lane == 0 ? (uint32_t)bits : (uint32_t)(bits >> 32);
         }
       }
     }
@@ -501,6 +657,24 @@ hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int MODE>
+static hipError_t launch_tile(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
+                              int64_t N, const Geom& g, long long* acc, uint32_t* out, hipStream_t s) {
+  const int64_t blocks = ((N + 255) / 256) * ((g.C + kTileC - 1) / kTileC);
+  const int grid = blocks < 65536 ? (int)blocks : 65536;
+  if (g.W <= 4)
+    tile_kernel<1, MODE><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
+  else if (g.W <= 16)
+    tile_kernel<4, MODE><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
+  else
+    tile_kernel<16, MODE><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
+  return hipGetLastError();
+}
+
+static bool tile_fits(const Geom& g, int mode) {
+  return g.P == 1 && g.W <= 64 && (mode == 1 || g.K <= kTileMaxK);
+}
+
 size_t score_lists_bytes(const Geom& g) {
   if (!literal_major(g) || g.L > 65535 || (size_t)(g.L * ((g.P + 31) / 32)) * 4 > 120 * 1024) return 0;
   return (size_t)g.C * kScoreListCap * 2 + (size_t)g.C * 4;
@@ -519,6 +693,7 @@ hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_
 
 hipError_t launch_score(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
                         int64_t N, const Geom& g, long long* acc, hipStream_t s) {
+  if (tile_fits(g, 0)) return launch_tile<0>(planes, ninc, w, X, N, g, acc, nullptr, s);
   if (g.P == 1 && g.K <= kScoreTileMaxK && (size_t)g.W * kScoreTile * 4 <= 48 * 1024) {
     const int64_t blocks = ((N + kScoreTile - 1) / kScoreTile) * ((g.C + kScoreTileChunk - 1) / kScoreTileChunk);
     const int grid = blocks < 65536 ? (int)blocks : 65536;
@@ -541,19 +716,37 @@ hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t 
 }
 
 hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const uint32_t* X, int64_t N,
-                            const Geom& g, int patchwise, uint32_t* out, hipStream_t s) {
+                            const Geom& g, int mode, uint32_t* out, hipStream_t s) {
+  if (tile_fits(g, 1)) return launch_tile<1>(planes, ninc, nullptr, X, N, g, nullptr, out, s);
   const int grid = grid_for(N * g.C * kWave, 256);
   if (g.P == 1) {
-    if (patchwise)
-      transform_kernel<true, true><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
-    else
-      transform_kernel<true, false><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
+    // One patch: per-patch output (packed or not) is the clause output.
+    transform_kernel<true, 0><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
+  } else if (mode == 0) {
+    transform_kernel<false, 0><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
+  } else if (mode == 1) {
+    transform_kernel<false, 1><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
   } else {
-    if (patchwise)
-      transform_kernel<false, true><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
-    else
-      transform_kernel<false, false><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
+    transform_kernel<false, 2><<<grid, 256, 0, s>>>(planes, ninc, X, N, g, out);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64_t N, const Geom& g, int mode,
+                               void* scratch, bool lists_ready, uint32_t* out, hipStream_t s) {
+  uint16_t* lists = (uint16_t*)scratch;
+  int32_t* nlit = (int32_t*)(lists + g.C * kScoreListCap);
+  if (!lists_ready)
+    build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
+  const int64_t blocks = N * ((g.C + kScoreLmChunk - 1) / kScoreLmChunk);
+  const int grid = blocks < 65536 ? (int)blocks : 65536;
+  const size_t lds = (size_t)(g.L * ((g.P + 31) / 32)) * 4;
+  if (mode == 0)
+    transform_lm_kernel<0><<<grid, 256, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+  else if (mode == 1)
+    transform_lm_kernel<1><<<grid, 256, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+  else
+    transform_lm_kernel<2><<<grid, 256, lds, s>>>(planes, lists, nlit, XT, N, g, out);
   return hipGetLastError();
 }
 
