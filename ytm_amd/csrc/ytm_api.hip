@@ -139,10 +139,6 @@ int upload(void** dst, const void* src, size_t bytes, hipStream_t s) {
   return YTM_OK;
 }
 
-// LDS a resident training workgroup may use (gfx950 has 160 KiB per workgroup; the
-// kernel's static LDS and some headroom are kept free).
-constexpr size_t kResidentLdsLimit = 150 * 1024;
-
 // Picks the persistent grid (one workgroup per CU at most, at least ~8 clauses each) and
 // the class-sum grouping (groups of <= 16 workgroups).
 void train_shape(int64_t C, int cus, int* grid, int* S, int* D, int* cpw) {
@@ -158,7 +154,12 @@ void train_shape(int64_t C, int cus, int* grid, int* S, int* D, int* cpw) {
   *cpw = (int)((C + G - 1) / G) + 1;
 }
 
-// The model geometry plus the launch shape of a training run on `cus` compute units.
+// The model geometry plus the launch shape of a training run on `cus` compute units:
+// one workgroup per CU with >= 8 clauses each, in class-sum exchange groups of 16.
+// Fewer, fuller workgroups do not pay: the exchange gets cheaper (about 1.0 us at 16
+// workgroups, 1.2 us at 32, 2.1 us at 250 on MI355X), but the per-sample evaluation and
+// draws then run on fewer CUs and take longer than that.  YTM_TRAIN_WGS / YTM_TRAIN_GROUP
+// / YTM_TRAIN_THREADS override.
 Geom train_geometry(const Geom& model, int cus, int* cpw) {
   int grid, S, D;
   train_shape(model.C, cus, &grid, &S, &D, cpw);
@@ -177,7 +178,7 @@ bool train_lds_fits(const Geom& g, ytm::TrainKind kind, int cpw, int cap) {
   Geom gc = g;
   gc.list_cap = cap;
   const int r = kind == ytm::TrainKind::kResident ? ytm::train_rng_slots(cpw, gc) : 0;
-  return ytm::train_lds_bytes(kind, cpw, r, gc) <= kResidentLdsLimit;
+  return ytm::train_lds_bytes(kind, cpw, r, gc) <= ytm::kResidentLdsLimit;
 }
 
 // Literal-list capacity of a training kernel kind (several patches): the resident kernel
@@ -491,7 +492,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.cpw = cpw;
     a.rng_slots = rng_slots;
     const char* prof_env = std::getenv("YTM_TRAIN_PROFILE");
-    a.profile = prof_env && std::atoi(prof_env) > 0;
+    a.profile = prof_env ? std::max(0, std::atoi(prof_env)) : 0;
     a.g = g;
     FIT_TRY(hipEventRecord(m->ev0, m->stream));
     if (jit_fn)

@@ -36,6 +36,10 @@ hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const u
 hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64_t N, const Geom& g, int mode,
                                void* scratch, bool lists_ready, uint32_t* out, hipStream_t s);
 
+// LDS a resident training workgroup may use (gfx950 has 160 KiB per workgroup; the
+// kernel's static LDS and some headroom are kept free).
+constexpr size_t kResidentLdsLimit = 150 * 1024;
+
 // Training kernel variants: clause state resident in LDS (one patch), or kept in global
 // memory (one patch / several patches).
 enum class TrainKind { kResident, kGlobalVanilla, kGlobalConv };

@@ -752,7 +752,9 @@ hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64
 
 int train_rng_slots(int cpw, const Geom& g) {
   const size_t per_slot = (size_t)g.W * kPreGroups * 4 * sizeof(uint32_t) + 2 * sizeof(int);
-  const size_t budget = 48 * 1024;
+  const size_t base = train_lds_bytes(TrainKind::kResident, cpw, 0, g);
+  const size_t left = base < kResidentLdsLimit ? kResidentLdsLimit - base : 0;
+  const size_t budget = std::min<size_t>(48 * 1024, left);
   return (int)std::max<size_t>(1, std::min<size_t>((size_t)cpw * g.K, budget / per_slot));
 }
 

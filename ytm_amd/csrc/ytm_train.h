@@ -454,6 +454,38 @@ __device__ FbOps decide(const TrainArgs& a, const Geom& g, const float* inj, int
   return FbOps{__ballot(t1a), __ballot(t1b), __ballot(t2)};
 }
 
+// The decision of decide() for one (clause, class) pair held by the calling lane (its own
+// clause c and class k), with the pre-drawn Q-skip and update draws uq, uu (or the
+// injected ones).  Not wave-uniform: every lane may hold another clause.
+struct PairOps {
+  bool t1a, t1b, t2;
+  float w_new;
+};
+
+template <bool INJECT>
+__device__ __forceinline__ PairOps decide_pair(const Geom& g, const float* inj, int64_t c, int64_t k, bool act, int sel,
+                                               int ninc, int tgt, double prob, float w0, float uq, float uu) {
+  if (INJECT) {
+    uq = inj[g.C * g.P + c * g.K + k];
+    uu = inj[g.C * g.P + g.C * g.K + c * g.K + k];
+  }
+  const bool o = sel >= 0;
+  const bool small = o && ninc <= g.maxinc;
+  const bool skip = tgt == -1 && (double)uq > g.q_prob;
+  const int sign = (w0 >= 0.0f) - (w0 < 0.0f);
+  const bool upd = act && !skip && (double)uu <= prob;
+  const int ts = tgt * sign;
+  PairOps r;
+  r.t1a = upd && ts > 0 && small;
+  r.t1b = upd && ts > 0 && !small;
+  r.t2 = upd && ts < 0 && o;
+  const float wa = w0 + (float)sign * 1.0f;
+  float wb = w0 - (float)sign * 1.0f;
+  if (!g.negative_polarity) wb = wb < 1.0f ? 1.0f : wb;
+  r.w_new = r.t1a ? wa : wb;
+  return r;
+}
+
 // Literal updates of one clause for the feedback decided in ops, applied class by class
 // in increasing k to the clause's planes (cplanes, stride W).  pre, when given, holds the
 // first kPreGroups plane groups of the literal draws of every Type Ia/Ib class, in the
@@ -579,6 +611,17 @@ __device__ void apply_tasks(const TrainArgs& a, const Geom& g, const float* inj,
   }
 }
 
+// Class k's clipped sum, feedback target and update probability from its exact total S
+// (kernel.cu:397,508-529,543-551).
+__device__ __forceinline__ void class_targets(const Geom& g, int k, long long S, const int32_t* y_row, int* s_tgt,
+                                              double* s_prob) {
+  const float cs = (float)S;
+  const float vclip = ((double)cs > g.thresh) ? (float)g.thresh : (((double)cs < -g.thresh) ? (float)(-g.thresh) : cs);
+  const int y = y_row[k];
+  s_tgt[k] = 1 - 2 * (vclip > (float)y);
+  s_prob[k] = ((double)y - (double)vclip) / (2.0 * (double)y);
+}
+
 // Phases B and C, run by wave 0 of every workgroup.  Per sample, a two-level all-reduce
 // of the K class sums with a broadcast back:
 //   1. lanes < K add (1<<44 | partial) into their group's word (groups of S workgroups);
@@ -605,6 +648,14 @@ __device__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, co
   unsigned long long* mbox = final_w + ks;                 // [D][ks]
   unsigned long long* poll = D == 1 ? group_w : mbox + d * ks;
   const unsigned long long poll_count = D == 1 ? gsize : (unsigned long long)D;
+  if (g.grid == 1) {  // one workgroup: its partial sums are the totals
+    if (lane < g.K) {
+      const long long part = s_part[lane];
+      s_part[lane] = 0;
+      class_targets(g, lane, part + (long long)bias[lane], y_row, s_tgt, s_prob);
+    }
+    return true;
+  }
   if (lane < g.K) {
     const long long part = s_part[lane];
     s_part[lane] = 0;
@@ -648,15 +699,7 @@ __device__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, co
     __builtin_amdgcn_s_sleep(1);
   }
   *wait_ticks += __builtin_amdgcn_s_memrealtime() - t_start;
-  if (lane < g.K) {
-    const int k = lane;
-    const long long S = (long long)(v - (poll_count << 44)) + (long long)bias[k];
-    const float cs = (float)S;
-    const float vclip = ((double)cs > g.thresh) ? (float)g.thresh : (((double)cs < -g.thresh) ? (float)(-g.thresh) : cs);
-    const int y = y_row[k];
-    s_tgt[k] = 1 - 2 * (vclip > (float)y);
-    s_prob[k] = ((double)y - (double)vclip) / (2.0 * (double)y);
-  }
+  if (lane < g.K) class_targets(g, lane, (long long)(v - (poll_count << 44)) + (long long)bias[lane], y_row, s_tgt, s_prob);
   return true;
 }
 
@@ -924,6 +967,74 @@ __device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g,
     atomicAdd((unsigned long long*)&part[kp], (unsigned long long)(long long)wk);
 }
 
+// Phase A of the one-patch clauses idx0, idx0 + stride, ... (below n_own) on sample j, by
+// one wave, kEvalBatch clauses at a time: every LDS read of a batch is issued before any
+// decision, and the batch's votes are summed in registers and added to part once.  The
+// per-clause results are those of resident_eval (eval_select with one patch).
+constexpr int kEvalBatch = 4;
+
+template <bool INJECT>
+__device__ void resident_eval_multi(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int idx0, int stride,
+                                    int n_own, const uint32_t* s_planes, const float* s_w, const int* s_drop,
+                                    const uint32_t* s_x, const float* s_usel, int* sel_out, int* ninc_out, int* s_pw,
+                                    long long* part) {
+  const int lane = lane_id();
+  const float* inj = INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr;
+  const bool exact_count = g.maxinc < g.L;
+  const uint32_t* x = s_x + (j % 3) * g.W;
+  const int64_t cw = (int64_t)g.np * g.W;
+  for (int r0 = idx0; r0 < n_own; r0 += kEvalBatch * stride) {
+    uint32_t bad[kEvalBatch], any[kEvalBatch];
+    int cnt[kEvalBatch];
+#pragma unroll
+    for (int b = 0; b < kEvalBatch; ++b) {
+      bad[b] = 0u;
+      any[b] = 0u;
+      cnt[b] = 0;
+    }
+    for (int64_t w = lane; w < g.W; w += kWave) {
+      const uint32_t nx = ~x[w];
+#pragma unroll
+      for (int b = 0; b < kEvalBatch; ++b) {
+        const int idx = r0 + b * stride;
+        if (idx < n_own) {
+          const uint32_t mw = s_planes[idx * cw + (int64_t)(g.np - 1) * g.W + w];
+          bad[b] |= mw & nx;
+          any[b] |= mw;
+          if (exact_count) cnt[b] += __popc(mw);
+        }
+      }
+    }
+    long long add = 0;  // lanes < K (coalesced): votes of the batch's selected clauses
+#pragma unroll
+    for (int b = 0; b < kEvalBatch; ++b) {
+      const int idx = r0 + b * stride;
+      if (idx >= n_own) continue;  // (no break: the loop must unroll for bad/any/cnt to stay in registers)
+      const int64_t c = c_begin + idx;
+      const int ninc = exact_count ? wave_sum_i32(cnt[b]) : (__any(any[b] != 0u) ? 1 : 0);
+      const bool any_bad = __any(bad[b] != 0u);
+      const float u = INJECT ? inj[c * g.P] : s_usel[(j % 3) * a.cpw + idx];
+      // a clause fires on its one patch when it is empty or matches; it is selected when
+      // its rank-1 draw is below 1.0f / 1 (eval_select)
+      const int sel = (s_drop[idx] != 0 || (ninc != 0 && any_bad) || !(u < 1.0f)) ? -1 : 0;
+      if (lane == 0) {
+        sel_out[idx] = sel;
+        ninc_out[idx] = ninc;
+        if (sel >= 0) s_pw[idx] += 1;
+      }
+      if (sel >= 0) {
+        if (g.coalesced) {
+          if (lane < g.K) add += (long long)s_w[idx * g.K + lane];
+        } else if (lane == 0) {
+          const int64_t kb = c / g.per_bank;
+          atomicAdd((unsigned long long*)&part[kb], (unsigned long long)(long long)s_w[idx * g.K + kb]);
+        }
+      }
+    }
+    if (g.coalesced && lane < g.K && add != 0) atomicAdd((unsigned long long*)&part[lane], (unsigned long long)add);
+  }
+}
+
 // Training with each workgroup's clause state resident in LDS for the whole launch:
 // planes [own][np][W], weights [own][K] (and, with one patch, patch weights [own]) are
 // loaded once, updated in place and written back at the end.  With several patches the
@@ -1007,6 +1118,18 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     s_spec_max = 0ull;
   }
   uint64_t spec_ticks = 0;  // profile: this wave's time in step 1 (waves >= 1)
+  // Register prefetch of the one-patch samples (see step 1 below): thread q of waves >= 1,
+  // counted from the last thread, holds word q (q < W) or target q - W (q < W + K).
+  const int q = (int)blockDim.x - 1 - (int)threadIdx.x;
+  const bool early = wave > 0 && g.P == 1 && g.W + g.K <= (int64_t)blockDim.x - kWave;
+  uint32_t xq = 0u;
+  int32_t yq = 0;
+  if (early && a.N > 2) {
+    if (q < g.W)
+      xq = a.X[2 * g.W + q];
+    else if (q < g.W + g.K)
+      yq = a.Y[2 * g.K + (q - g.W)];
+  }
   __syncthreads();
   if (cap > 0) {
     for (int idx = wave; idx < n_own; idx += nwv) {
@@ -1016,10 +1139,15 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     __syncthreads();
   }
   // Phase A of sample 0, every wave.
-  if (a.N > 0)
-    for (int idx = wave; idx < n_own; idx += nwv)
-      resident_eval<INJECT>(a, g, 0, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, s_sel, s_ninc, s_pw,
-                            s_part[0]);
+  if (a.N > 0) {
+    if (g.P == 1)
+      resident_eval_multi<INJECT>(a, g, 0, c_begin, wave, nwv, n_own, s_planes, s_w, s_drop, s_x, s_usel, s_sel, s_ninc,
+                                  s_pw, s_part[0]);
+    else
+      for (int idx = wave; idx < n_own; idx += nwv)
+        resident_eval<INJECT>(a, g, 0, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, s_sel, s_ninc,
+                              s_pw, s_part[0]);
+  }
   __syncthreads();
   prof_last = __builtin_amdgcn_s_memrealtime();
 
@@ -1041,61 +1169,145 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       YTM_PROF_MARK(0);
     } else {
       const uint64_t spec_t0 = a.profile ? __builtin_amdgcn_s_memrealtime() : 0;
-      if (more)
-        for (int idx = wave - 1; idx < n_own; idx += nwv - 1)
-          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, s_sel + b2n * cpw,
-                                s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+      // One patch: sample i+2 was read from global memory one iteration ago (one word or
+      // target per thread of the last waves); it goes to LDS now, and sample i+3 is read
+      // into the same registers, so no wait on the read latency remains.
+      if (early) {
+        if (i + 2 < a.N) {
+          if (q < g.W)
+            s_x[((i + 2) % 3) * g.W + q] = xq;
+          else if (q < g.W + g.K)
+            s_y[((i + 2) % 3) * g.K + (q - g.W)] = yq;
+        }
+        if (i + 3 < a.N) {
+          if (q < g.W)
+            xq = a.X[(int64_t)(i + 3) * g.W + q];
+          else if (q < g.W + g.K)
+            yq = a.Y[(int64_t)(i + 3) * g.K + (q - g.W)];
+        }
+      }
+      if (more) {
+        if (g.P == 1)
+          resident_eval_multi<INJECT>(a, g, i + 1, c_begin, wave - 1, nwv - 1, n_own, s_planes, s_w, s_drop, s_x, s_usel,
+                                      s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+        else
+          for (int idx = wave - 1; idx < n_own; idx += nwv - 1)
+            resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit,
+                                  s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+      }
+      if (a.profile == 2) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
       if (i + 2 < a.N) {
         const int b3nn = (i + 2) % 3;
-        stage_sample(a, g, i + 2, b3nn, s_x, s_y, threadIdx.x - kWave, blockDim.x - kWave);
+        if (!early) stage_sample(a, g, i + 2, b3nn, s_x, s_y, threadIdx.x - kWave, blockDim.x - kWave);
+        if (a.profile == 3) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
         if (g.P > 1) stage_xt(a, g, i + 2, b2, s_xt, threadIdx.x - kWave, blockDim.x - kWave);
         if (!INJECT)
           precompute_draws(a, g, i + 2, b3nn, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x - kWave,
                            blockDim.x - kWave);
       }
-      if (a.profile) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
+      if (a.profile == 1) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
     }
     __syncthreads();
     YTM_PROF_MARK(1);
     if (s_abort) break;
 
-    // ---- D1: each wave decides its own clauses' feedback, takes back the speculative
-    // votes of the clauses that change, and queues them
-    for (int idx = wave; idx < n_own; idx += nwv) {
-      const int64_t c = c_begin + idx;
-      const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
-      const float wold = s_w[idx * g.K + kp];
-      const FbOps ops = decide<INJECT, !INJECT>(a, g, inj, c, t, s_sel[b2 * cpw + idx], s_ninc[b2 * cpw + idx], s_tgt,
-                                                s_prob, s_w + idx * g.K, s_uq + ((int64_t)b3 * cpw + idx) * g.K,
-                                                s_uu + ((int64_t)b3 * cpw + idx) * g.K, s_drop[idx] != 0);
-      if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
-      const int spec_sel = more ? s_sel[b2n * cpw + idx] : -1;
-      if (spec_sel >= 0) {
-        if (g.coalesced ? lane < g.K : lane == 0)
-          atomicAdd((unsigned long long*)&s_part[b2n][kp], (unsigned long long)(-(long long)wold));
+    // ---- D1: feedback decisions of sample i; the clauses that change take back their
+    // speculative votes of sample i+1 and are queued.  With at most one clause per wave,
+    // each wave decides its clause (decide, lanes = classes); with more, lanes take
+    // (clause, class) pairs, kn classes per clause and 64 / kn clauses per wave pass
+    // (decide_pair), and a clause is queued by its first lane.
+    if (n_own <= nwv) {
+      for (int idx = wave; idx < n_own; idx += nwv) {
+        const int64_t c = c_begin + idx;
+        const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
+        const float wold = s_w[idx * g.K + kp];
+        const FbOps ops = decide<INJECT, !INJECT>(a, g, inj, c, t, s_sel[b2 * cpw + idx], s_ninc[b2 * cpw + idx], s_tgt,
+                                                  s_prob, s_w + idx * g.K, s_uq + ((int64_t)b3 * cpw + idx) * g.K,
+                                                  s_uu + ((int64_t)b3 * cpw + idx) * g.K, s_drop[idx] != 0);
+        if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
+        const int spec_sel = more ? s_sel[b2n * cpw + idx] : -1;
+        if (spec_sel >= 0) {
+          if (g.coalesced ? lane < g.K : lane == 0)
+            atomicAdd((unsigned long long*)&s_part[b2n][kp], (unsigned long long)(-(long long)wold));
+          if (lane == 0) {
+            if (g.P == 1)
+              s_pw[idx] -= 1;
+            else
+              atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
+          }
+        }
         if (lane == 0) {
-          if (g.P == 1)
-            s_pw[idx] -= 1;
-          else
-            atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
+          ++my_updates;
+          const unsigned long long rng = INJECT ? 0ull : (ops.m1a | ops.m1b);
+          const int tk = atomicAdd(&s_ntask, 1);
+          const int sb = INJECT ? 0 : atomicAdd(&s_nslot, __popcll(rng));
+          s_task_idx[tk] = idx;
+          s_task_sb[tk] = sb;
+          s_task_m[tk * 3 + 0] = ops.m1a;
+          s_task_m[tk * 3 + 1] = ops.m1b;
+          s_task_m[tk * 3 + 2] = ops.m2;
+          const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+          int j = sb;
+          for (unsigned long long r = rng; r; r &= r - 1ull, ++j) {
+            if (j < R) {
+              s_slot_idx[j] = idx;
+              s_slot_k[j] = (int)(kb + __ffsll((long long)r) - 1);
+            }
+          }
         }
       }
-      if (lane == 0) {
-        ++my_updates;
-        const unsigned long long rng = INJECT ? 0ull : (ops.m1a | ops.m1b);
-        const int tk = atomicAdd(&s_ntask, 1);
-        const int sb = INJECT ? 0 : atomicAdd(&s_nslot, __popcll(rng));
-        s_task_idx[tk] = idx;
-        s_task_sb[tk] = sb;
-        s_task_m[tk * 3 + 0] = ops.m1a;
-        s_task_m[tk * 3 + 1] = ops.m1b;
-        s_task_m[tk * 3 + 2] = ops.m2;
-        const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
-        int j = sb;
-        for (unsigned long long r = rng; r; r &= r - 1ull, ++j) {
-          if (j < R) {
-            s_slot_idx[j] = idx;
-            s_slot_k[j] = (int)(kb + __ffsll((long long)r) - 1);
+    } else {
+      const int kn = g.coalesced ? (int)g.K : 1;
+      const int cpp = kWave / kn;  // clauses per pass
+      const int jc = lane / kn, kk = lane - jc * kn;
+      const unsigned long long seg = kn == kWave ? ~0ull : ((1ull << kn) - 1ull);
+      for (int base = wave * cpp; base < n_own; base += nwv * cpp) {
+        const int idx = base + jc;
+        const bool valid = jc < cpp && idx < n_own;
+        const int ix = valid ? idx : base;  // idle lanes read a valid clause and discard it
+        const int64_t c = c_begin + ix;
+        const int64_t k = (g.coalesced ? 0 : c / g.per_bank) + kk;
+        float* wp = s_w + (int64_t)ix * g.K + k;
+        const float wold = *wp;
+        const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && s_drop[ix] == 0, s_sel[b2 * cpw + ix],
+                                               s_ninc[b2 * cpw + ix], s_tgt[k], s_prob[k], wold,
+                                               s_uq[((int64_t)b3 * cpw + ix) * g.K + k],
+                                               s_uu[((int64_t)b3 * cpw + ix) * g.K + k]);
+        if (po.t1a || po.t2) *wp = po.w_new;
+        const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
+        if ((b1a | b1b | bt2) == 0ull) continue;
+        const int sh = jc * kn;
+        const unsigned long long m1a = valid ? (b1a >> sh) & seg : 0ull;
+        const unsigned long long m1b = valid ? (b1b >> sh) & seg : 0ull;
+        const unsigned long long m2 = valid ? (bt2 >> sh) & seg : 0ull;
+        const bool changes = (m1a | m1b | m2) != 0ull;
+        const int spec_sel = more && changes ? s_sel[b2n * cpw + ix] : -1;
+        if (spec_sel >= 0)
+          atomicAdd((unsigned long long*)&s_part[b2n][k], (unsigned long long)(-(long long)wold));
+        const bool leader = changes && kk == 0;
+        my_updates += (unsigned long long)__popcll(__ballot(leader));
+        if (leader) {
+          if (spec_sel >= 0) {
+            if (g.P == 1)
+              s_pw[ix] -= 1;
+            else
+              atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
+          }
+          const unsigned long long rng = INJECT ? 0ull : (m1a | m1b);
+          const int tk = atomicAdd(&s_ntask, 1);
+          const int sb = INJECT ? 0 : atomicAdd(&s_nslot, __popcll(rng));
+          s_task_idx[tk] = ix;
+          s_task_sb[tk] = sb;
+          s_task_m[tk * 3 + 0] = m1a;
+          s_task_m[tk * 3 + 1] = m1b;
+          s_task_m[tk * 3 + 2] = m2;
+          const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+          int jj = sb;
+          for (unsigned long long r = rng; r; r &= r - 1ull, ++jj) {
+            if (jj < R) {
+              s_slot_idx[jj] = ix;
+              s_slot_k[jj] = (int)(kb + __ffsll((long long)r) - 1);
+            }
           }
         }
       }
