@@ -139,11 +139,14 @@ int upload(void** dst, const void* src, size_t bytes, hipStream_t s) {
   return YTM_OK;
 }
 
-// Picks the persistent grid (one workgroup per CU at most, at least ~8 clauses each) and
-// the class-sum grouping (groups of <= 16 workgroups).
+// Picks the persistent grid (one workgroup per CU at most, at least ~12 clauses each, and
+// two workgroups for models of more than one clause) and the class-sum grouping (groups of
+// <= 16 workgroups).  ~12 clauses per workgroup balance the per-sample exchange, which
+// gets slower with more workgroups, against the per-workgroup evaluation and draws (config
+// 2 on MI355X: 167 workgroups train 2.7% faster than 250, and 96-192 are within 1%).
 void train_shape(int64_t C, int cus, int* grid, int* S, int* D, int* cpw) {
   const char* env = std::getenv("YTM_TRAIN_WGS");
-  int64_t G = std::min<int64_t>(cus, std::max<int64_t>(1, (C + 7) / 8));
+  int64_t G = std::min<int64_t>(cus, std::max<int64_t>(std::min<int64_t>(C, 2), (C + 11) / 12));
   if (env && std::atoi(env) > 0) G = std::min<int64_t>(std::atoi(env), C);
   *grid = (int)G;
   const char* envs = std::getenv("YTM_TRAIN_GROUP");
@@ -154,8 +157,8 @@ void train_shape(int64_t C, int cus, int* grid, int* S, int* D, int* cpw) {
   *cpw = (int)((C + G - 1) / G) + 1;
 }
 
-// The model geometry plus the launch shape of a training run on `cus` compute units:
-// one workgroup per CU with >= 8 clauses each, in class-sum exchange groups of 16.
+// The model geometry plus the launch shape of a training run on `cus` compute units
+// (train_shape).
 // Fewer, fuller workgroups do not pay: the exchange gets cheaper (about 1.0 us at 16
 // workgroups, 1.2 us at 32, 2.1 us at 250 on MI355X), but the per-sample evaluation and
 // draws then run on fewer CUs and take longer than that.  YTM_TRAIN_WGS / YTM_TRAIN_GROUP
