@@ -27,6 +27,19 @@ enum {
     YTM_ERANGE = 4    /* state value outside what the model can represent */
 };
 
+/* Element types of the binarizer inputs (ytm_binarize). */
+enum {
+    YTM_DTYPE_U8 = 0,
+    YTM_DTYPE_I8 = 1,
+    YTM_DTYPE_U16 = 2,
+    YTM_DTYPE_I16 = 3,
+    YTM_DTYPE_U32 = 4,
+    YTM_DTYPE_I32 = 5,
+    YTM_DTYPE_I64 = 6,
+    YTM_DTYPE_F32 = 7,
+    YTM_DTYPE_F64 = 8
+};
+
 /* Model hyperparameters, resolved on the host exactly as src/cutm/base.py:60-121,129-152
  * resolves them into #defines.  s_inv and q_prob are S_INV and Q_PROB as the reference's
  * C preprocessor types them (float or double, kernel.cu:31-32), widened to double. */
@@ -150,6 +163,24 @@ int ytm_set_weights(ytm_model *m, const float *in);
 int ytm_get_patch_weights(ytm_model *m, int32_t *out);
 int ytm_set_patch_weights(ytm_model *m, const int32_t *in);
 int ytm_get_bias(ytm_model *m, float *out);
+
+/* ---- Host preprocessing: the binarizers of src/tm_utils/binarizer.py (no model needed).
+ *
+ * ytm_binarize replaces the transform of Binarizer (binarizer.py:63-86, 107-113) and the
+ * binarize_gray / binarize_rgb of ThermometerBinarizer (binarizer.py:9-22): X holds n values
+ * of type x_dtype (YTM_DTYPE_*), thresholds nthr values, int64 when int_thresholds else
+ * double.  Comparisons are made in int64 when X and the thresholds are integers, else in
+ * double (numpy's promotion for these operands).
+ *   kind 0, thermometer: out uint32 (n, nthr), out[i][j] = X[i] >= t[j];
+ *   kind 1, one-hot: out uint32 (n, nthr - 1 + 2 * edge_bins); the nthr - 1 intervals
+ *           t[j] <= X[i] < t[j + 1], preceded by X[i] < t[0] and followed by
+ *           X[i] >= t[nthr - 1] when edge_bins.
+ * ytm_collapse_bins replaces Binarizer.collapse_bins (binarizer.py:88-129): B uint32
+ * (rows, width) -> out int64 (rows): kind 0, the index of the last non-zero value + 1 (0 if
+ * none); kind 1, the index of the first maximum; minus 1 when edge_bins. */
+int ytm_binarize(const void *X, int x_dtype, int64_t n, const void *thresholds, int int_thresholds, int nthr,
+                 int kind, int edge_bins, uint32_t *out);
+int ytm_collapse_bins(const uint32_t *B, int64_t rows, int64_t width, int kind, int edge_bins, int64_t *out);
 
 #ifdef __cplusplus
 }

@@ -84,7 +84,14 @@ SIGNATURES = {
     "ytm_get_patch_weights": (ctypes.c_int, [_P, _P]),
     "ytm_set_patch_weights": (ctypes.c_int, [_P, _P]),
     "ytm_get_bias": (ctypes.c_int, [_P, _P]),
+    "ytm_binarize": (ctypes.c_int, [_P, ctypes.c_int, _I64, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    _P]),
+    "ytm_collapse_bins": (ctypes.c_int, [_P, _I64, _I64, ctypes.c_int, ctypes.c_int, _P]),
 }
+
+# Element types of ytm_binarize (YTM_DTYPE_* of include/ytm.h).
+DTYPES = {"uint8": 0, "int8": 1, "uint16": 2, "int16": 3, "uint32": 4, "int32": 5, "int64": 6, "float32": 7,
+          "float64": 8}
 
 
 def _load() -> ctypes.CDLL:

@@ -704,3 +704,78 @@ int ytm_get_bias(ytm_model* m, float* out) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- binarizers
+namespace {
+
+size_t dtype_size(int dtype) {
+  switch (dtype) {
+    case YTM_DTYPE_U8:
+    case YTM_DTYPE_I8:
+      return 1;
+    case YTM_DTYPE_U16:
+    case YTM_DTYPE_I16:
+      return 2;
+    case YTM_DTYPE_U32:
+    case YTM_DTYPE_I32:
+    case YTM_DTYPE_F32:
+      return 4;
+    case YTM_DTYPE_I64:
+    case YTM_DTYPE_F64:
+      return 8;
+    default:
+      return 0;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ytm_binarize(const void* X, int x_dtype, int64_t n, const void* thresholds, int int_thresholds, int nthr,
+                 int kind, int edge_bins, uint32_t* out) {
+  const size_t es = dtype_size(x_dtype);
+  if (es == 0) return fail(YTM_EINVAL, "unsupported binarizer input type");
+  if (kind != 0 && kind != 1) return fail(YTM_EINVAL, "binarizer kind must be 0 (thermometer) or 1 (one-hot)");
+  if (n < 0 || nthr < (kind == 1 ? 2 : 1) || !thresholds || (n > 0 && (!X || !out)))
+    return fail(YTM_EINVAL, "bad binarizer arguments");
+  if (int_thresholds && (x_dtype == YTM_DTYPE_F32 || x_dtype == YTM_DTYPE_F64))
+    return fail(YTM_EINVAL, "integer thresholds need integer input");
+  const int64_t width = kind == 0 ? nthr : nthr - 1 + (edge_bins ? 2 : 0);
+  if (n == 0) return YTM_OK;
+  void* dX = nullptr;
+  void* dT = nullptr;
+  uint32_t* dO = nullptr;
+  int rc = upload(&dX, X, (size_t)n * es, nullptr);
+  if (!rc) rc = upload(&dT, thresholds, (size_t)nthr * 8, nullptr);
+  hipError_t e = hipSuccess;
+  if (!rc) e = hipMalloc(&dO, (size_t)(n * width) * 4);
+  if (!rc && e == hipSuccess)
+    e = ytm::launch_binarize(dX, x_dtype, n, dT, int_thresholds != 0, nthr, kind == 1, edge_bins != 0, dO, nullptr);
+  if (!rc && e == hipSuccess) e = hipMemcpy(out, dO, (size_t)(n * width) * 4, hipMemcpyDeviceToHost);
+  if (!rc && e != hipSuccess) rc = fail(YTM_EHIP, std::string("binarize failed: ") + hipGetErrorString(e));
+  if (dX) (void)hipFree(dX);
+  if (dT) (void)hipFree(dT);
+  if (dO) (void)hipFree(dO);
+  return rc;
+}
+
+int ytm_collapse_bins(const uint32_t* B, int64_t rows, int64_t width, int kind, int edge_bins, int64_t* out) {
+  if (kind != 0 && kind != 1) return fail(YTM_EINVAL, "binarizer kind must be 0 (thermometer) or 1 (one-hot)");
+  if (rows < 0 || width < 0 || (rows > 0 && (!B || !out))) return fail(YTM_EINVAL, "bad collapse arguments");
+  if (rows == 0) return YTM_OK;
+  void* dB = nullptr;
+  int64_t* dO = nullptr;
+  int rc = upload(&dB, B, (size_t)(rows * width) * 4, nullptr);
+  hipError_t e = hipSuccess;
+  if (!rc) e = hipMalloc(&dO, (size_t)rows * 8);
+  if (!rc && e == hipSuccess)
+    e = ytm::launch_collapse_bins((const uint32_t*)dB, rows, width, kind == 1, edge_bins != 0, dO, nullptr);
+  if (!rc && e == hipSuccess) e = hipMemcpy(out, dO, (size_t)rows * 8, hipMemcpyDeviceToHost);
+  if (!rc && e != hipSuccess) rc = fail(YTM_EHIP, std::string("collapse_bins failed: ") + hipGetErrorString(e));
+  if (dB) (void)hipFree(dB);
+  if (dO) (void)hipFree(dO);
+  return rc;
+}
+
+}  // extern "C"

@@ -6,6 +6,7 @@
 #include <string>
 #include <vector>
 
+#include "ytm.h"
 #include "ytm_types.h"
 
 namespace ytm {
@@ -35,6 +36,13 @@ hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const u
 // built first unless lists_ready.
 hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64_t N, const Geom& g, int mode,
                                void* scratch, bool lists_ready, uint32_t* out, hipStream_t s);
+
+// Binarizers (host preprocessing): element-wise thermometer / one-hot binning and the
+// collapse of binned rows; see ytm_binarize / ytm_collapse_bins in ytm.h.
+hipError_t launch_binarize(const void* X, int dtype, int64_t n, const void* t, bool int_thresholds, int nthr,
+                           bool onehot, int edge, uint32_t* out, hipStream_t s);
+hipError_t launch_collapse_bins(const uint32_t* B, int64_t rows, int64_t width, bool onehot, int edge, int64_t* out,
+                                hipStream_t s);
 
 // LDS a resident training workgroup may use (gfx950 has 160 KiB per workgroup; the
 // kernel's static LDS and some headroom are kept free).
