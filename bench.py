@@ -22,6 +22,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+# VALU 32-bit lane-ops per second: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz (MI355X).
+VALU_PEAK_T = 256 * 4 * 16 * 2.4e9 / 1e12
 
 
 def log(msg: str) -> None:
@@ -35,6 +37,11 @@ def train_bytes_per_launch(tm, samples: int, updates: int) -> float:
     C, K, L = tm.number_of_clauses, tm.number_of_outputs, tm.number_of_literals
     P, W = tm.number_of_patches, tm.number_of_literal_chunks
     return float((samples * C + updates) * (2 * L + 4 * K) + samples * 4 * P * W)
+
+
+def infer_word_ands(tm, samples: int) -> float:
+    """Inference VALU work: every clause tested on every patch, C*P*W word-ANDs per sample."""
+    return float(samples) * tm.number_of_clauses * tm.number_of_patches * tm.number_of_literal_chunks
 
 
 def infer_bytes(tm, samples: int) -> float:
@@ -237,6 +244,14 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": load_traffic(cfg),
+        },
+        "infer_roofline": {
+            "bound": "valu",
+            "achieved": round(infer_word_ands(tm, Nt) / (inf_kern / 1e3) / 1e12, 3),
+            "peak": round(VALU_PEAK_T, 2),
+            "unit": "T word-ANDs/s (C*P*W 32-bit lane-ops per sample, no early exit)",
+            "frac": round(infer_word_ands(tm, Nt) / (inf_kern / 1e3) / 1e12 / VALU_PEAK_T, 4),
+            "hbm_gbs": round(infer_bytes(tm, Nt) / (inf_kern / 1e3) / 1e9, 2),
         },
         "cpu_baseline": None,
     }

@@ -31,6 +31,9 @@ struct ytm_model {
   int* d_err = nullptr;
   unsigned long long* d_slots = nullptr;
   size_t slots_bytes = 0;
+  // Upper bound of |clause weight|: 1 after initialisation, the largest loaded magnitude
+  // after ytm_set_weights, and + 1 per trained sample (a sample moves a weight by at most 1).
+  double w_bound = 1.0;
   ytm_stats stats;
 };
 
@@ -468,6 +471,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   FIT_TRY(hipMemsetAsync(m->d_err, 0, 16, m->stream));
   double ms_total = 0.0;
   int launches = 0;
+  m->w_bound += (double)count;  // before any launch: also holds if one fails part-way
   for (int64_t s = 0; s < count; s += per_launch) {
     const int64_t n = std::min(per_launch, count - s);
     if (inj)
@@ -554,18 +558,26 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   float* dout = nullptr;
   void* lists = nullptr;  // several patches: the clauses' literal lists
   const size_t lists_bytes = ds->d_XT ? ytm::score_lists_bytes(g) : 0;
-  HIP_TRY(hipMalloc(&acc, (size_t)(N * g.K) * 8));
+  const int64_t chunks = lists_bytes ? 0 : ytm::score_tile_chunks(g);  // one patch: per-chunk sums
+  HIP_TRY(hipMalloc(&acc, (size_t)(N * g.K * (chunks ? chunks : 1)) * 8));
   hipError_t e = hipMalloc(&dout, (size_t)(N * g.K) * 4);
   if (e == hipSuccess && lists_bytes) e = hipMalloc(&lists, lists_bytes);
   int rc = YTM_OK;
   if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
-  if (e == hipSuccess) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
+  if (e == hipSuccess && !chunks) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
   if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
-  if (e == hipSuccess)
-    e = lists ? ytm::launch_score_lm(m->d_planes, m->d_w, ds->d_XT, N, g, lists, acc, m->stream)
-              : ytm::launch_score(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->stream);
+  if (e == hipSuccess) {
+    if (lists)
+      e = ytm::launch_score_lm(m->d_planes, m->d_w, ds->d_XT, N, g, lists, acc, m->stream);
+    else if (chunks)
+      e = ytm::launch_score_tile(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->w_bound, m->stream);
+    else
+      e = ytm::launch_score(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->stream);
+  }
   if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
-  if (e == hipSuccess) e = ytm::launch_score_finish(acc, m->d_bias, N, g, dout, m->stream);
+  if (e == hipSuccess)
+    e = chunks ? ytm::launch_score_parts_finish(acc, chunks, m->d_bias, N, g, dout, m->stream)
+               : ytm::launch_score_finish(acc, m->d_bias, N, g, dout, m->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(class_sums, dout, (size_t)(N * g.K) * 4, hipMemcpyDeviceToHost, m->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
   float ms = 0.0f;
@@ -679,6 +691,9 @@ int ytm_set_weights(ytm_model* m, const float* in) {
   }
   HIP_TRY(hipMemcpyAsync(m->d_w, in, (size_t)(m->g.C * m->g.K) * 4, hipMemcpyHostToDevice, m->stream));
   HIP_TRY(hipStreamSynchronize(m->stream));
+  double bound = 0.0;
+  for (int64_t i = 0; i < m->g.C * m->g.K; ++i) bound = std::max(bound, (double)std::fabs(in[i]));
+  m->w_bound = bound;
   return YTM_OK;
 }
 

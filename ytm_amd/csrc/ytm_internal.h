@@ -19,8 +19,18 @@ hipError_t launch_planes_to_ta(const uint32_t* planes, uint32_t* ta, const Geom&
 hipError_t launch_init_state(uint32_t* planes, float* w, const Geom& g, uint64_t seed, hipStream_t s);
 hipError_t launch_ninc(const uint32_t* planes, int32_t* ninc, const Geom& g, hipStream_t s);
 hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s);
+// Class-sum accumulation into acc int64 [N][K] (zeroed by the caller).
 hipError_t launch_score(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
                         int64_t N, const Geom& g, long long* acc, hipStream_t s);
+// One-patch models: the tiled scorer writes per-chunk sums parts int64 [chunks][N][K]
+// (chunks = score_tile_chunks(g), 0 when the tiled scorer does not apply), which
+// launch_score_parts_finish adds up with the bias.  w_bound: an upper bound of |weight|,
+// which lets the kernel sum in int32 when that is exact.
+int64_t score_tile_chunks(const Geom& g);
+hipError_t launch_score_tile(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
+                             int64_t N, const Geom& g, long long* parts, double w_bound, hipStream_t s);
+hipError_t launch_score_parts_finish(const long long* parts, int64_t nch, const float* bias, int64_t N, const Geom& g,
+                                     float* out, hipStream_t s);
 // Scoring of several-patch models on literal-major samples; scratch holds score_lists_bytes(g)
 // (0: not available for this geometry).
 size_t score_lists_bytes(const Geom& g);

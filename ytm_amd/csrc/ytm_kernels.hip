@@ -6,6 +6,8 @@
 //   patch_w int32  [C][P]       reservoir selection counts
 // Encoded inputs keep the reference layout uint32 [N][P][W] (src/cutm/base.py:238).
 #include <algorithm>
+#include <cstdlib>
+#include <type_traits>
 
 #include "ytm_device.h"
 #include "ytm_internal.h"
@@ -399,6 +401,18 @@ __global__ __launch_bounds__(256) void score_lm_kernel(const uint32_t* __restric
   }
 }
 
+// Class sums from per-chunk slices parts[nch][N][K] (tile_kernel) plus the bias.
+__global__ __launch_bounds__(256) void score_parts_finish_kernel(const long long* __restrict__ parts, int64_t nch,
+                                                                 const float* __restrict__ bias, int64_t N, Geom g,
+                                                                 float* __restrict__ out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < N * g.K;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    long long v = (long long)bias[i % g.K];
+    for (int64_t ch = 0; ch < nch; ++ch) v += parts[ch * N * g.K + i];
+    out[i] = (float)v;
+  }
+}
+
 __global__ __launch_bounds__(256) void score_finish_kernel(const long long* __restrict__ acc,
                                                            const float* __restrict__ bias, int64_t N,
                                                            Geom g, float* __restrict__ out) {
@@ -415,16 +429,18 @@ __global__ __launch_bounds__(256) void score_finish_kernel(const long long* __re
 // vote); MODE 1 writes clause outputs (transform, kernel.cu:346-368, and transform_patchwise
 // with its single patch: empty clauses output 1) through per-clause ballots in LDS, so that
 // each output row is written coalesced.  MAXQ bounds W by 4*MAXQ words.
-constexpr int kTileC = 128;
+constexpr int kTileC = 96;
 constexpr int kTileMaxK = 16;
 
-template <int MAXQ, int MODE>
+template <int MAXQ, int MODE, bool SUM32>
 __global__ __launch_bounds__(256) void tile_kernel(const uint32_t* __restrict__ planes,
                                                    const int32_t* __restrict__ ninc, const float* __restrict__ w,
                                                    const uint32_t* __restrict__ X, int64_t N, Geom g,
                                                    long long* __restrict__ acc, uint32_t* __restrict__ out) {
+  // SUM32: the class sums of a chunk are exact in int32 (the caller bounds |w| * kTileC < 2^31)
+  using Sum = typename std::conditional<SUM32, int, long long>::type;
   __shared__ uint4 s_m[kTileC * MAXQ];
-  __shared__ long long s_w[MODE == 0 ? kTileC * kTileMaxK : 1];
+  __shared__ Sum s_w[MODE == 0 ? kTileC * kTileMaxK : 1];
   __shared__ int s_live[kTileC];
   __shared__ unsigned long long s_bal[MODE == 1 ? 4 * kTileC : 1];
   const int lane = lane_id();
@@ -442,51 +458,59 @@ __global__ __launch_bounds__(256) void tile_kernel(const uint32_t* __restrict__ 
     }
     for (int j = threadIdx.x; j < nc; j += blockDim.x) s_live[j] = ninc[c0 + j] != 0;
     if (MODE == 0)
-      for (int j = threadIdx.x; j < nc * (int)g.K; j += blockDim.x) s_w[j] = (long long)w[c0 * g.K + j];
+      for (int j = threadIdx.x; j < nc * (int)g.K; j += blockDim.x) s_w[j] = (Sum)w[c0 * g.K + j];
     const int64_t e = e0 + lane;
     uint32_t nx[4 * MAXQ];
 #pragma unroll
     for (int ww = 0; ww < 4 * MAXQ; ++ww) nx[ww] = (ww < g.W && e < N) ? ~X[e * g.W + ww] : 0u;
-    long long sum[MODE == 0 ? kTileMaxK : 1];
+    Sum sum[MODE == 0 ? kTileMaxK : 1];
 #pragma unroll
     for (int k = 0; k < (MODE == 0 ? kTileMaxK : 1); ++k) sum[k] = 0;
     __syncthreads();
     for (int cl = 0; cl < nc; ++cl) {
       const uint4* row = s_m + cl * MAXQ;
-      // Groups of up to 16 words: the group's LDS reads are issued together, and the wave
-      // stops once none of its samples can satisfy the clause.
-      uint32_t bad = 0u;
+      // Groups of up to 16 words: the group's LDS reads are issued together, the words go
+      // into two independent AND-OR chains, and the wave stops once none of its samples can
+      // satisfy the clause.
+      uint32_t bad0 = 0u, bad1 = 0u;
 #pragma unroll
       for (int q0 = 0; q0 < MAXQ; q0 += 4) {
-        if (q0 < Wq && (q0 == 0 || __any(bad == 0u))) {
+        if (q0 < Wq && (q0 == 0 || __any((bad0 | bad1) == 0u))) {
           uint4 mv[MAXQ < 4 ? MAXQ : 4];
 #pragma unroll
           for (int u = 0; u < (MAXQ < 4 ? MAXQ : 4); ++u) mv[u] = row[q0 + u];
 #pragma unroll
           for (int u = 0; u < (MAXQ < 4 ? MAXQ : 4); ++u) {
             const int b = 4 * (q0 + u);
-            bad |= (mv[u].x & nx[b]) | (mv[u].y & nx[b + 1]) | (mv[u].z & nx[b + 2]) | (mv[u].w & nx[b + 3]);
+            bad0 |= mv[u].x & nx[b];
+            bad1 |= mv[u].y & nx[b + 1];
+            bad0 |= mv[u].z & nx[b + 2];
+            bad1 |= mv[u].w & nx[b + 3];
           }
         }
       }
+      const bool match = (bad0 | bad1) == 0u;
       const bool live = s_live[cl] != 0;
       if (MODE == 0) {
-        const bool fire = live && bad == 0u;
+        const bool fire = live && match;
         if (__any(fire)) {
 #pragma unroll
           for (int k = 0; k < kTileMaxK; ++k)
-            if (k < g.K) sum[k] += fire ? s_w[cl * g.K + k] : 0ll;
+            if (k < g.K) sum[k] += fire ? s_w[cl * g.K + k] : (Sum)0;
         }
       } else {
-        const unsigned long long bits = __ballot(!live || bad == 0u);
+        const unsigned long long bits = __ballot(!live || match);
         if (lane == 0) s_bal[wave * kTileC + cl] = bits;
       }
     }
     if (MODE == 0) {
+      // the chunk's sums, stored (every value, zeros included) into its own slice
+      // acc[chunk][N][K]; score_parts_finish_kernel adds the slices
       if (e < N) {
+        long long* dst = acc + ((blk % nch) * N + e) * g.K;
 #pragma unroll
         for (int k = 0; k < kTileMaxK; ++k)
-          if (k < g.K && sum[k] != 0) atomicAdd((unsigned long long*)&acc[e * g.K + k], (unsigned long long)sum[k]);
+          if (k < g.K) dst[k] = (long long)sum[k];
       }
     } else {
       __syncthreads();  // the ballots are complete
@@ -657,17 +681,17 @@ hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int MODE>
+template <int MODE, bool SUM32>
 static hipError_t launch_tile(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
                               int64_t N, const Geom& g, long long* acc, uint32_t* out, hipStream_t s) {
   const int64_t blocks = ((N + 255) / 256) * ((g.C + kTileC - 1) / kTileC);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
   if (g.W <= 4)
-    tile_kernel<1, MODE><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
+    tile_kernel<1, MODE, SUM32><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
   else if (g.W <= 16)
-    tile_kernel<4, MODE><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
+    tile_kernel<4, MODE, SUM32><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
   else
-    tile_kernel<16, MODE><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
+    tile_kernel<16, MODE, SUM32><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc, out);
   return hipGetLastError();
 }
 
@@ -691,9 +715,23 @@ hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_
   return hipGetLastError();
 }
 
+int64_t score_tile_chunks(const Geom& g) { return tile_fits(g, 0) ? (g.C + kTileC - 1) / kTileC : 0; }
+
+hipError_t launch_score_tile(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
+                             int64_t N, const Geom& g, long long* parts, double w_bound, hipStream_t s) {
+  const bool sum32 = w_bound * kTileC < 2147483648.0;
+  return sum32 ? launch_tile<0, true>(planes, ninc, w, X, N, g, parts, nullptr, s)
+               : launch_tile<0, false>(planes, ninc, w, X, N, g, parts, nullptr, s);
+}
+
+hipError_t launch_score_parts_finish(const long long* parts, int64_t nch, const float* bias, int64_t N, const Geom& g,
+                                     float* out, hipStream_t s) {
+  score_parts_finish_kernel<<<grid_for(N * g.K, 256), 256, 0, s>>>(parts, nch, bias, N, g, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_score(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
                         int64_t N, const Geom& g, long long* acc, hipStream_t s) {
-  if (tile_fits(g, 0)) return launch_tile<0>(planes, ninc, w, X, N, g, acc, nullptr, s);
   if (g.P == 1 && g.K <= kScoreTileMaxK && (size_t)g.W * kScoreTile * 4 <= 48 * 1024) {
     const int64_t blocks = ((N + kScoreTile - 1) / kScoreTile) * ((g.C + kScoreTileChunk - 1) / kScoreTileChunk);
     const int grid = blocks < 65536 ? (int)blocks : 65536;
@@ -717,7 +755,7 @@ hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t 
 
 hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const uint32_t* X, int64_t N,
                             const Geom& g, int mode, uint32_t* out, hipStream_t s) {
-  if (tile_fits(g, 1)) return launch_tile<1>(planes, ninc, nullptr, X, N, g, nullptr, out, s);
+  if (tile_fits(g, 1)) return launch_tile<1, false>(planes, ninc, nullptr, X, N, g, nullptr, out, s);
   const int grid = grid_for(N * g.C * kWave, 256);
   if (g.P == 1) {
     // One patch: per-patch output (packed or not) is the clause output.

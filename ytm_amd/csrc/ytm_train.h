@@ -723,6 +723,47 @@ __device__ __forceinline__ void add_partial(const TrainArgs& a, const Geom& g, l
     prof_last = now_;                                         \
   }
 
+// Copies n words from global memory to LDS, threads [first, first + count) taking part,
+// with up to kCopyBatch reads of each thread in flight before its LDS writes (a plain copy
+// loop waits for every read in turn).  8-byte copies when n is even (both buffers are then
+// 8-byte aligned).
+constexpr int kCopyBatch = 8;
+
+__device__ __forceinline__ void copy_to_lds(uint32_t* dst, const uint32_t* src, int64_t n, int first, int count) {
+  if ((n & 1) == 0) {
+    const uint2* s2 = (const uint2*)src;
+    uint2* d2 = (uint2*)dst;
+    const int64_t n2 = n / 2;
+    for (int64_t j0 = first; j0 < n2; j0 += (int64_t)count * kCopyBatch) {
+      uint2 v[kCopyBatch];
+#pragma unroll
+      for (int b = 0; b < kCopyBatch; ++b) {
+        const int64_t j = j0 + (int64_t)b * count;
+        if (j < n2) v[b] = s2[j];
+      }
+#pragma unroll
+      for (int b = 0; b < kCopyBatch; ++b) {
+        const int64_t j = j0 + (int64_t)b * count;
+        if (j < n2) d2[j] = v[b];
+      }
+    }
+  } else {
+    for (int64_t j0 = first; j0 < n; j0 += (int64_t)count * kCopyBatch) {
+      uint32_t v[kCopyBatch];
+#pragma unroll
+      for (int b = 0; b < kCopyBatch; ++b) {
+        const int64_t j = j0 + (int64_t)b * count;
+        if (j < n) v[b] = src[j];
+      }
+#pragma unroll
+      for (int b = 0; b < kCopyBatch; ++b) {
+        const int64_t j = j0 + (int64_t)b * count;
+        if (j < n) dst[j] = v[b];
+      }
+    }
+  }
+}
+
 // Clause state in global memory (L2/MALL resident across samples); any P.
 template <bool VANILLA, bool INJECT>
 __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom& g) {
@@ -772,13 +813,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     if (!VANILLA && literal_major(g)) {
       xt = a.XT + (int64_t)i * xt_words;
       if (literal_major_lds(g)) {
-        if ((xt_words & 1) == 0) {  // 8-byte copies: s_xt and every sample start are 8-byte aligned
-          const uint2* src = (const uint2*)xt;
-          uint2* dst = (uint2*)s_xt;
-          for (int64_t j = threadIdx.x; j < xt_words / 2; j += blockDim.x) dst[j] = src[j];
-        } else {
-          for (int64_t j = threadIdx.x; j < xt_words; j += blockDim.x) s_xt[j] = xt[j];
-        }
+        copy_to_lds(s_xt, xt, xt_words, threadIdx.x, blockDim.x);
         xt = s_xt;
       }
     }
@@ -911,18 +946,11 @@ __device__ __forceinline__ void precompute_draws(const TrainArgs& a, const Geom&
 }
 
 // Copies the literal-major sample i ([L][PW] words) into LDS buffer buf of s_xt, threads
-// [first, first + count) taking part (8-byte copies when the word count is even: s_xt and
-// every sample start are then 8-byte aligned).
+// [first, first + count) taking part.
 __device__ __forceinline__ void stage_xt(const TrainArgs& a, const Geom& g, int i, int buf, uint32_t* s_xt, int first,
                                          int count) {
   const int64_t n = g.L * ((g.P + 31) / 32);
-  const uint32_t* src = a.XT + (int64_t)i * n;
-  uint32_t* dst = s_xt + (int64_t)buf * n;
-  if ((n & 1) == 0) {
-    for (int64_t j = first; j < n / 2; j += count) ((uint2*)dst)[j] = ((const uint2*)src)[j];
-  } else {
-    for (int64_t j = first; j < n; j += count) dst[j] = src[j];
-  }
+  copy_to_lds(s_xt + (int64_t)buf * n, a.XT + (int64_t)i * n, n, first, count);
 }
 
 // Phase A of one resident clause (local index idx) on sample j, by one wave: selection
