@@ -163,6 +163,36 @@ def test_fit_variant_flags(opts):
     assert_state_equal(tm, ref, str(opts))
 
 
+@pytest.mark.parametrize("case", [
+    dict(dim=(16, 1, 1), n_classes=64, clauses=64, n=160),                           # 64 classes: a lane per class
+    dict(dim=(20, 1, 1), n_classes=3, clauses=40, n=120, number_of_ta_states=65535),  # 16 state bit-planes
+    dict(dim=(66, 66, 1), patch_dim=(3, 3), n_classes=2, clauses=16, n=3),            # 4096 patches (no literal-major copy)
+])
+def test_supported_limits(case):
+    """Training, scores and clause outputs at the largest sizes resolve_geometry accepts."""
+    case = dict(case)
+    n, clauses = case.pop("n"), case.pop("clauses")
+    kw = dict(number_of_clauses_per_class=clauses, T=20, s=3.0, seed=5, **case)
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(clauses, 20, 3.0, kw["dim"], kw["n_classes"],
+                       **{k: v for k, v in kw.items() if k in ("patch_dim", "number_of_ta_states", "seed")})
+    rng = np.random.default_rng(17)
+    X = (rng.random((n, int(np.prod(kw["dim"])))) < 0.5).astype(np.uint32)
+    y = rng.integers(0, kw["n_classes"], size=n).astype(np.uint32)
+    encX = tm.encode(X)
+    np.testing.assert_array_equal(encX, ref.encode(X))
+    for epoch in range(2):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+    np.testing.assert_array_equal(tm.score(encX, is_X_encoded=True), ref.score(encX))
+    np.testing.assert_array_equal(tm.transform(encX, is_X_encoded=True), ref.transform(encX))
+    ref_pw = ref.transform(encX[:2], patchwise=True)
+    np.testing.assert_array_equal(tm.transform_patchwise(encX[:2], is_X_encoded=True), ref_pw)
+    assert_packed_equal(tm.transform_patchwise(encX[:2], is_X_encoded=True, packed=True), ref_pw)
+
+
 def test_fit_conv_variant_no_loc():
     tm, ref, X, y, *_ = pair(3, 30, clauses=50, encode_loc=False)
     encX = tm.encode(X)
