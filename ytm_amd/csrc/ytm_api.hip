@@ -199,6 +199,16 @@ int train_list_cap(const Geom& g, ytm::TrainKind kind, int cpw) {
 
 // Keeps the workgroup's clause state resident in LDS when it fits (with several patches,
 // together with two literal-major samples), else the global kernel; sets g->list_cap.
+// A one-patch model on the global kernel keeps its include masks (and the sample) in LDS
+// when they fit (g->mask_lds).
+void set_mask_lds(Geom* g, ytm::TrainKind kind, int cpw) {
+  g->mask_lds = 0;
+  if (kind == ytm::TrainKind::kGlobalVanilla) {
+    g->mask_lds = 1;
+    if (!train_lds_fits(*g, kind, cpw, 0)) g->mask_lds = 0;
+  }
+}
+
 ytm::TrainKind choose_train_kind(Geom* g, int cpw, bool force_global) {
   ytm::TrainKind kind = g->P == 1 ? ytm::TrainKind::kGlobalVanilla : ytm::TrainKind::kGlobalConv;
   if (!force_global && (g->P == 1 || ytm::literal_major(*g))) {
@@ -206,6 +216,7 @@ ytm::TrainKind choose_train_kind(Geom* g, int cpw, bool force_global) {
     if (train_lds_fits(*g, ytm::TrainKind::kResident, cpw, cap)) kind = ytm::TrainKind::kResident;
   }
   g->list_cap = train_list_cap(*g, kind, cpw);
+  set_mask_lds(g, kind, cpw);
   return kind;
 }
 
@@ -289,6 +300,7 @@ int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injec
   if (!valid)
     return fail(YTM_EINVAL, "train_kind 1 is for one patch, 2 for several, 0 for one patch or a literal-major model");
   g.list_cap = train_list_cap(g, (ytm::TrainKind)train_kind, cpw);
+  set_mask_lds(&g, (ytm::TrainKind)train_kind, cpw);
   std::vector<char> code;
   std::string why;
   if (!ytm::jit_compile(g, (ytm::TrainKind)train_kind, injected != 0, &code, &why))

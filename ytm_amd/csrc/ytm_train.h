@@ -492,14 +492,17 @@ __device__ __forceinline__ PairOps decide_pair(const Geom& g, const float* inj, 
 // order of those classes: [op][W][kPreGroups][4].
 template <bool INJECT>
 __device__ void apply_ops(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, int sel, FbOps ops,
-                          uint32_t* cplanes, const uint32_t* xe, const uint32_t* pre) {
+                          uint32_t* cplanes, const uint32_t* xe, const uint32_t* pre, uint32_t* top_copy = nullptr,
+                          int64_t wb_first = 0, int64_t wb_end = -1) {
+  // words [wb_first, wb_end) of the clause (wb_first a multiple of 64; wb_end < 0: to W)
   const int lane = lane_id();
   const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
   const bool o = sel >= 0;
   const uint32_t* xsel = o ? xe + (int64_t)sel * g.W : nullptr;
   const int np = g.np;
   const unsigned long long all = ops.m1a | ops.m1b | ops.m2;
-  for (int64_t wb = 0; wb < g.W; wb += kWave) {
+  const int64_t wend = wb_end < 0 || wb_end > g.W ? g.W : wb_end;
+  for (int64_t wb = wb_first; wb < wend; wb += kWave) {
     const int64_t w = wb + lane;
     const bool act = w < g.W;
     const uint32_t F = act ? (w == g.W - 1 ? g.last_filter : 0xFFFFFFFFu) : 0u;
@@ -534,6 +537,7 @@ __device__ void apply_ops(const TrainArgs& a, const Geom& g, const float* inj, i
 #pragma unroll
       for (int j = 0; j < kMaxPlanes; ++j)
         if (j < np) pw[(int64_t)j * g.W] = pl[j];
+      if (top_copy) top_copy[w] = pl[np - 1];  // the include mask, also kept in LDS
     }
   }
 }
@@ -557,7 +561,7 @@ template <bool INJECT>
 __device__ void apply_tasks(const TrainArgs& a, const Geom& g, const float* inj, int64_t c_begin, uint64_t t, int tk0,
                             int per, int ntask, const int* s_task_idx, const unsigned long long* s_task_m,
                             const int* s_task_sb, const int* sel_of, uint32_t* planes_base, const uint32_t* xe,
-                            const uint32_t* s_rng, int R) {
+                            const uint32_t* s_rng, int R, uint32_t* top_base = nullptr) {
   const int lane = lane_id();
   const int W = (int)g.W;
   const int grp = lane / W, w = lane % W;
@@ -608,6 +612,7 @@ __device__ void apply_tasks(const TrainArgs& a, const Geom& g, const float* inj,
 #pragma unroll
     for (int j = 0; j < kMaxPlanes; ++j)
       if (j < np) pw[(int64_t)j * W] = pl[j];
+    if (top_base) top_base[(int64_t)idx * W + w] = pl[np - 1];  // include masks kept in LDS ([idx][W])
   }
 }
 
@@ -790,6 +795,11 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   uint32_t* s_xt = (uint32_t*)(s_lits + (int64_t)a.cpw * cap);  // [L][PW] when literal_major_lds(g)
   const int64_t cw = (int64_t)g.np * g.W;
   const int64_t xt_words = literal_major(g) ? g.L * ((g.P + 31) / 32) : 0;
+  // mask_lds (one patch): the own clauses' include masks [cpw][W], kept current by the
+  // literal updates, and the current sample [W]
+  uint32_t* s_mask = s_xt + (literal_major_lds(g) ? xt_words : 0);
+  uint32_t* s_xs = s_mask + (g.mask_lds ? (int64_t)a.cpw * g.W : 0);
+  float* s_wg = (float*)(s_xs + (g.mask_lds ? g.W : 0));  // the own clauses' weights [cpw][K]
   unsigned long long my_updates = 0ull;
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
@@ -798,6 +808,11 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   uint64_t prof_last = t_kernel;
   if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_abort = 0;
+  for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) s_wg[j] = a.weights[c_begin * g.K + j];
+  if (g.mask_lds)  // include masks of the own clauses (visible after the first barrier below)
+    for (int idx = wave; idx < n_own; idx += (int)(blockDim.x / kWave))
+      for (int64_t w = lane; w < g.W; w += kWave)
+        s_mask[(int64_t)idx * g.W + w] = a.planes[(c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W + w];
   if (cap > 0)  // literal lists of the own clauses (visible after the first barrier below)
     for (int idx = wave; idx < n_own; idx += (int)(blockDim.x / kWave)) {
       const int n = build_literal_list(g, a.planes + (c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W,
@@ -809,6 +824,10 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     const uint64_t t = a.step0 + (uint64_t)i;
     const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
     const uint32_t* xe = a.X + (int64_t)i * g.P * g.W;
+    if (g.mask_lds) {
+      copy_to_lds(s_xs, xe, g.W, threadIdx.x, blockDim.x);
+      xe = s_xs;
+    }
     const uint32_t* xt = nullptr;  // literal-major sample
     if (!VANILLA && literal_major(g)) {
       xt = a.XT + (int64_t)i * xt_words;
@@ -828,7 +847,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       if (idx >= n_own) break;
       const int64_t c = c_begin + idx;
       int ninc;
-      const uint32_t* m = a.planes + (c * g.np + g.np - 1) * g.W;
+      const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : a.planes + (c * g.np + g.np - 1) * g.W;
       const int sel = (!VANILLA && literal_major(g))
                           ? eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * cap,
                                                    cap > 0 ? s_nlit[idx] : 0, cap, xt, a.drop[c] == 1u, &ninc)
@@ -839,7 +858,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       }
       if (sel >= 0) {
         if (lane == 0) a.patch_w[c * g.P + sel] += 1;
-        add_partial(a, g, s_part, c, a.weights + c * g.K);
+        add_partial(a, g, s_part, c, s_wg + (int64_t)idx * g.K);
       }
     }
     YTM_PROF_MARK(0);
@@ -869,7 +888,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       const int64_t c = c_begin + idx;
       if (a.drop[c] == 1u) continue;
       const FbOps ops = decide<INJECT, false>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob,
-                                              a.weights + c * g.K, nullptr, nullptr);
+                                              s_wg + (int64_t)idx * g.K, nullptr, nullptr);
       if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
       if (lane == 0) {
         ++my_updates;
@@ -880,16 +899,30 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         s_task_m[tk * 3 + 1] = ops.m1b;
         s_task_m[tk * 3 + 2] = ops.m2;
       }
-      if (g.W > 32) apply_ops<INJECT>(a, g, inj, c, t, s_sel[idx], ops, a.planes + c * cw, xe, nullptr);
     }
-    if (g.W <= 32) {
-      __syncthreads();
+    __syncthreads();
+    {
       const int ntask = s_ntask;
       const int nwv = (int)(blockDim.x / kWave);
-      const int per = tasks_per_wave(g, ntask, nwv);
-      for (int tk0 = wave * per; tk0 < ntask; tk0 += nwv * per)
-        apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb, s_sel,
-                            a.planes + c_begin * cw, xe, nullptr, 0);
+      if (g.W <= 32) {
+        // narrow clauses: up to 64 / W queued updates per wave at once
+        const int per = tasks_per_wave(g, ntask, nwv);
+        for (int tk0 = wave * per; tk0 < ntask; tk0 += nwv * per)
+          apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb, s_sel,
+                              a.planes + c_begin * cw, xe, nullptr, 0, g.mask_lds ? s_mask : nullptr);
+      } else {
+        // wide clauses: (update, 64-word chunk) items over all waves; the chunks of one
+        // clause touch disjoint literals
+        const int nchunk = (int)((g.W + kWave - 1) / kWave);
+        for (int item = wave; item < ntask * nchunk; item += nwv) {
+          const int tk = item / nchunk, ch = item - tk * nchunk;
+          const int idx = s_task_idx[tk];
+          const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
+          apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[idx], ops, a.planes + (c_begin + idx) * cw, xe, nullptr,
+                            g.mask_lds ? s_mask + (int64_t)idx * g.W : nullptr, (int64_t)ch * kWave,
+                            (int64_t)(ch + 1) * kWave);
+        }
+      }
     }
     YTM_PROF_MARK(4);
     __syncthreads();
@@ -904,6 +937,8 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     }
     YTM_PROF_MARK(5);
   }
+  __syncthreads();
+  for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) a.weights[c_begin * g.K + j] = s_wg[j];
   if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
   if (threadIdx.x == 0) {
     atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
