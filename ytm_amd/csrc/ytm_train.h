@@ -206,13 +206,52 @@ __device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* li
 }
 
 // Firing bitmap of a clause from its literal list (n literals, padded to a multiple of 8)
-// on the literal-major sample xt: acc AND-ed with the bitsets of the listed literals, 8 per
-// step (two 8-byte reads of the list, the same for every lane); stops once nothing fires.
-// list must be 8-byte aligned.
+// on the literal-major sample xt: acc (lane j: patch word j < PW, the all-patches mask)
+// AND-ed with the bitsets of the listed literals, 8 per step (two 8-byte reads of the
+// list); stops once nothing fires.  When at least two groups of PW lanes fit in the wave,
+// each group walks its own runs of 8 literals and the groups' bitmaps are AND-ed at the
+// end, so one step covers 8 * (64 / PW) literals.  list must be 8-byte aligned.
 __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16_t* list, int n, const uint32_t* xt,
                                                      uint32_t acc) {
   const int lane = lane_id();
   const int PW = (int)((g.P + 31) / 32);
+  const int NG = kWave / PW;  // lane groups of PW lanes
+  if (NG >= 2) {
+    // Group q (lanes [q*PW, (q+1)*PW)) ANDs the literal runs 8q, 8q + 8*NG, ... into its own
+    // partial bitmap (lane q*PW + w: word w); a group whose partial is empty everywhere ends
+    // the walk, and the groups' partials are AND-ed together at the end.
+    const int q = lane / PW, w = lane - q * PW;
+    const bool in_group = q < NG;
+    // word w of the all-patches mask
+    uint32_t part = in_group ? (w == PW - 1 && (g.P & 31) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu) : 0u;
+    const unsigned long long gmask = PW >= 64 ? ~0ull : ((1ull << PW) - 1ull);
+    for (int j0 = 0; j0 < n; j0 += 8 * NG) {
+      const int j = j0 + 8 * q;
+      if (in_group && j < n) {
+        const uint2 q0 = *(const uint2*)(list + j), q1 = *(const uint2*)(list + j + 4);
+        const uint32_t w8[4] = {q0.x, q0.y, q1.x, q1.y};
+        uint32_t v = 0xFFFFFFFFu;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)w];
+          v &= xt[(w8[u] >> 16) * (uint32_t)PW + (uint32_t)w];
+        }
+        part &= v;
+      }
+      const unsigned long long live = __ballot(part != 0u);
+      bool dead = false;
+      for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * PW)) & gmask) == 0ull;
+      if (dead) {
+        part = 0u;
+        break;
+      }
+    }
+    // AND of the groups' partials: lane w (< PW) gathers word w of every group
+    uint32_t r = part;
+    for (int gq = 1; gq < NG; ++gq)
+      r &= (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (w + gq * PW < kWave ? w + gq * PW : lane), (int)part);
+    return lane < PW ? (r & acc) : 0u;
+  }
   const int jl = lane < PW ? lane : 0;
   for (int j = 0; j < n; j += 8) {
     const uint2 q0 = *(const uint2*)(list + j), q1 = *(const uint2*)(list + j + 4);
