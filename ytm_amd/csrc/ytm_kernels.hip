@@ -333,21 +333,60 @@ __global__ __launch_bounds__(256) void build_lists_kernel(const uint32_t* __rest
 }
 
 // Firing bitmap from a literal list held in registers: lane q has entries [8q, 8q + 8) in
-// lv (the list padded to a multiple of 8), read 8 at a time with readlane.
+// lv (the list padded to a multiple of 8).  With at least two groups of PW lanes in the wave
+// (the bitmap's PW words), group gq takes the runs 8(it * NG + gq) of step it, fetching
+// them from their lanes with ds_bpermute, and the groups' bitmaps are AND-ed at the end
+// (as firing_from_list); otherwise the runs are read 8 at a time with readlane.
 __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 lv, int n, const uint32_t* xt,
                                                           uint32_t acc) {
   const int lane = lane_id();
   const int PW = (int)((g.P + 31) / 32);
+  const int NG = kWave / PW;
+  if (NG >= 2) {
+    const int q = lane / PW, w = lane - q * PW;
+    const bool in_group = q < NG;
+    uint32_t part = in_group ? (w == PW - 1 && (g.P & 31) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu) : 0u;
+    const unsigned long long gmask = (1ull << PW) - 1ull;
+    const int nruns = (n + 7) / 8;
+    for (int r0 = 0; r0 < nruns; r0 += NG) {
+      const int run = r0 + (in_group ? q : 0);
+      const int src = 4 * (run < kWave ? run : 0);
+      const uint32_t e[4] = {(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.x),
+                             (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.y),
+                             (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.z),
+                             (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.w)};
+      if (in_group && run < nruns) {
+        uint32_t v = 0xFFFFFFFFu;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          v &= xt[(e[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)w];
+          v &= xt[(e[u] >> 16) * (uint32_t)PW + (uint32_t)w];
+        }
+        part &= v;
+      }
+      const unsigned long long live = __ballot(part != 0u);
+      bool dead = false;
+      for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * PW)) & gmask) == 0ull;
+      if (dead) {
+        part = 0u;
+        break;
+      }
+    }
+    uint32_t r = part;
+    for (int gq = 1; gq < NG; ++gq)
+      r &= (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (w + gq * PW < kWave ? w + gq * PW : lane), (int)part);
+    return lane < PW ? (r & acc) : 0u;
+  }
   const int jl = lane < PW ? lane : 0;
   for (int j = 0; j < n; j += 8) {
     const int src = j >> 3;
-    const uint32_t q[4] = {(uint32_t)lane_value((int)lv.x, src), (uint32_t)lane_value((int)lv.y, src),
-                           (uint32_t)lane_value((int)lv.z, src), (uint32_t)lane_value((int)lv.w, src)};
+    const uint32_t qv[4] = {(uint32_t)lane_value((int)lv.x, src), (uint32_t)lane_value((int)lv.y, src),
+                            (uint32_t)lane_value((int)lv.z, src), (uint32_t)lane_value((int)lv.w, src)};
     uint32_t v = 0xFFFFFFFFu;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      v &= xt[(q[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)jl];
-      v &= xt[(q[u] >> 16) * (uint32_t)PW + (uint32_t)jl];
+      v &= xt[(qv[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)jl];
+      v &= xt[(qv[u] >> 16) * (uint32_t)PW + (uint32_t)jl];
     }
     acc &= v;
     if ((j & 8) && !__any(acc != 0u)) break;
