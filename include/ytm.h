@@ -88,7 +88,9 @@ typedef struct ytm_stats {
                                     training kernel (resident: exchange, barrier, D1, barrier,
                                     D2, D3, barrier, and the slowest other wave's time in the
                                     exchange step; global: A, barrier, exchange, barrier, D,
-                                    barrier) */
+                                    barrier).  YTM_TRAIN_PROFILE=2 / =3 restrict that last
+                                    resident slot to the next sample's evaluation / its
+                                    evaluation and the staging of the sample after it */
 } ytm_stats;
 
 /* Thread-local description of the last failure. */
