@@ -655,19 +655,31 @@ __device__ void apply_tasks(const TrainArgs& a, const Geom& g, const float* inj,
   }
 }
 
-// Class k's clipped sum, feedback target and update probability from its exact total S
-// (kernel.cu:397,508-529,543-551).
-__device__ __forceinline__ void class_targets(const Geom& g, int k, long long S, const int32_t* y_row, int* s_tgt,
-                                              double* s_prob) {
+// Feedback target and update probability of one class.
+struct ClassFb {
+  int tgt;
+  double prob;
+};
+
+// Class feedback from the class's exact total S and target y (kernel.cu:397,508-529,543-551):
+// the sum clipped to +-T, target -1 when the clipped sum exceeds y, and the update
+// probability (y - clip) / (2y) in double.
+__device__ __forceinline__ ClassFb class_fb(const Geom& g, long long S, int y) {
   const float cs = (float)S;
   const float vclip = ((double)cs > g.thresh) ? (float)g.thresh : (((double)cs < -g.thresh) ? (float)(-g.thresh) : cs);
-  const int y = y_row[k];
-  s_tgt[k] = 1 - 2 * (vclip > (float)y);
-  s_prob[k] = ((double)y - (double)vclip) / (2.0 * (double)y);
+  return ClassFb{1 - 2 * (vclip > (float)y), ((double)y - (double)vclip) / (2.0 * (double)y)};
 }
 
-// Phases B and C, run by wave 0 of every workgroup.  Per sample, a two-level all-reduce
-// of the K class sums with a broadcast back:
+// class_fb of class k, stored to s_tgt[k] / s_prob[k].
+__device__ __forceinline__ void class_targets(const Geom& g, int k, long long S, const int32_t* y_row, int* s_tgt,
+                                              double* s_prob) {
+  const ClassFb r = class_fb(g, S, y_row[k]);
+  s_tgt[k] = r.tgt;
+  s_prob[k] = r.prob;
+}
+
+// Per sample, a two-level all-reduce of the K class sums over the grid, with a broadcast
+// back (phases B/C, run by wave 0 of every workgroup):
 //   1. lanes < K add (1<<44 | partial) into their group's word (groups of S workgroups);
 //   2. for each word, the adder that completes its group (returned count == group size)
 //      forwards the group total into the final word;
@@ -675,57 +687,78 @@ __device__ __forceinline__ void class_targets(const Geom& g, int k, long long S,
 //      stores the total into every group's mailbox;
 //   4. each workgroup polls its own group's mailbox (bounded in real time).
 // Contention stays at <= S adders / pollers per word.  With one group the group words are
-// polled directly.  Lanes < K then derive clip / target / update probability
-// (kernel.cu:397,508-529,543-551).  Returns false when the wait expired.
-__device__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, const int32_t* y_row, const float* bias,
-                                    long long* s_part, int* s_tgt, double* s_prob, int* s_abort,
-                                    uint64_t* wait_ticks) {
-  const int lane = lane_id();
-  const int wg = blockIdx.x;
+// polled directly; with one workgroup its partial sums are the totals.
+struct ExchangeRow {
+  unsigned long long* group_w;  // [D][ks]
+  unsigned long long* final_w;  // [ks]
+  unsigned long long* mbox;     // [D][ks]
+  unsigned long long* poll;     // the words this workgroup waits on
+  unsigned long long gsize;     // workgroups in this workgroup's group
+  unsigned long long poll_count;
+  int d, ks;
+};
+
+__device__ __forceinline__ ExchangeRow exchange_row(const TrainArgs& a, const Geom& g, int i) {
+  ExchangeRow r;
   const int D = g.groups;
-  const int d = wg / g.group_size;
-  const unsigned long long gsize = (unsigned long long)min(g.group_size, g.grid - d * g.group_size);
-  const int ks = ((int)g.K + 15) & ~15;                    // words per row (128-byte multiples)
+  r.d = (int)blockIdx.x / g.group_size;
+  r.gsize = (unsigned long long)min(g.group_size, g.grid - r.d * g.group_size);
+  r.ks = ((int)g.K + 15) & ~15;  // words per row (128-byte multiples)
   unsigned long long* row = a.slots + (int64_t)i * a.slot_stride;
-  unsigned long long* group_w = row;                       // [D][ks]
-  unsigned long long* final_w = row + D * ks;            // [ks]
-  unsigned long long* mbox = final_w + ks;                 // [D][ks]
-  unsigned long long* poll = D == 1 ? group_w : mbox + d * ks;
-  const unsigned long long poll_count = D == 1 ? gsize : (unsigned long long)D;
-  if (g.grid == 1) {  // one workgroup: its partial sums are the totals
-    if (lane < g.K) {
-      const long long part = s_part[lane];
-      s_part[lane] = 0;
-      class_targets(g, lane, part + (long long)bias[lane], y_row, s_tgt, s_prob);
+  r.group_w = row;
+  r.final_w = row + D * r.ks;
+  r.mbox = r.final_w + r.ks;
+  r.poll = D == 1 ? r.group_w : r.mbox + r.d * r.ks;
+  r.poll_count = D == 1 ? r.gsize : (unsigned long long)D;
+  return r;
+}
+
+// Steps 1-3: lanes < K publish the workgroup's partial sums of sample i (s_part, cleared;
+// with one workgroup they stay in s_part for exchange_wait).
+__device__ __forceinline__ void exchange_publish(const TrainArgs& a, const Geom& g, int i, long long* s_part) {
+  const int lane = lane_id();
+  if (g.grid == 1 || lane >= g.K) return;
+  const ExchangeRow r = exchange_row(a, g, i);
+  const long long part = s_part[lane];
+  s_part[lane] = 0;
+  const unsigned long long mine = (1ull << 44) + (unsigned long long)part;
+  if (g.groups == 1) {
+    __hip_atomic_fetch_add(&r.group_w[lane], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    const unsigned long long now =
+        __hip_atomic_fetch_add(&r.group_w[r.d * r.ks + lane], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    if (((now + (1ull << 43)) >> 44) == r.gsize) {
+      const unsigned long long fwd = (1ull << 44) + (now - (r.gsize << 44));
+      const unsigned long long now2 =
+          __hip_atomic_fetch_add(&r.final_w[lane], fwd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + fwd;
+      if (((now2 + (1ull << 43)) >> 44) == (unsigned long long)g.groups)
+        for (int m = 0; m < g.groups; ++m)
+          __hip_atomic_store(&r.mbox[m * r.ks + lane], now2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+}
+
+// Step 4: the whole wave waits until the total of every class is in; lanes with want set
+// return the total of class kq (< K) in *S.  Returns false when the wait expired (s_abort
+// and a.err record it).  With one workgroup the totals are read from s_part, which is then
+// cleared.
+__device__ __forceinline__ bool exchange_wait(const TrainArgs& a, const Geom& g, int i, int kq, bool want,
+                                              long long* s_part, long long* S, int* s_abort, uint64_t* wait_ticks) {
+  const int lane = lane_id();
+  if (g.grid == 1) {
+    if (want) *S = s_part[kq];
+    __builtin_amdgcn_wave_barrier();  // every read of s_part before it is cleared
+    if (lane < g.K) s_part[lane] = 0;
     return true;
   }
-  if (lane < g.K) {
-    const long long part = s_part[lane];
-    s_part[lane] = 0;
-    const unsigned long long mine = (1ull << 44) + (unsigned long long)part;
-    if (D == 1) {
-      __hip_atomic_fetch_add(&group_w[lane], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      const unsigned long long now =
-          __hip_atomic_fetch_add(&group_w[d * ks + lane], mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
-      if (((now + (1ull << 43)) >> 44) == gsize) {
-        const unsigned long long fwd = (1ull << 44) + (now - (gsize << 44));
-        const unsigned long long now2 =
-            __hip_atomic_fetch_add(&final_w[lane], fwd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + fwd;
-        if (((now2 + (1ull << 43)) >> 44) == (unsigned long long)D)
-          for (int m = 0; m < D; ++m)
-            __hip_atomic_store(&mbox[m * ks + lane], now2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
+  const ExchangeRow r = exchange_row(a, g, i);
   const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
   unsigned long long v = 0;
   for (;;) {
     bool ok = true;
-    if (lane < g.K) {
-      v = __hip_atomic_load(&poll[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok = ((v + (1ull << 43)) >> 44) == poll_count;
+    if (want) {
+      v = __hip_atomic_load(&r.poll[kq], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = ((v + (1ull << 43)) >> 44) == r.poll_count;
     }
     if (__all(ok)) break;
     if (__builtin_amdgcn_s_memrealtime() - t_start > kWaitTicks) {
@@ -734,7 +767,7 @@ __device__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, co
         *s_abort = 1;
         if (atomicCAS(a.err, 0, 1) == 0) {
           a.err[1] = i;
-          a.err[2] = wg;
+          a.err[2] = (int)blockIdx.x;
           a.err[3] = (int)((v + (1ull << 43)) >> 44);
         }
       }
@@ -743,7 +776,20 @@ __device__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, co
     __builtin_amdgcn_s_sleep(1);
   }
   *wait_ticks += __builtin_amdgcn_s_memrealtime() - t_start;
-  if (lane < g.K) class_targets(g, lane, (long long)(v - (poll_count << 44)) + (long long)bias[lane], y_row, s_tgt, s_prob);
+  if (want) *S = (long long)(v - (r.poll_count << 44));
+  return true;
+}
+
+// The whole exchange of sample i; lanes < K then derive clip / target / update probability
+// into s_tgt / s_prob.  Returns false when the wait expired.
+__device__ __forceinline__ bool exchange_class_sums(const TrainArgs& a, const Geom& g, int i, const int32_t* y_row,
+                                                    const float* bias, long long* s_part, int* s_tgt, double* s_prob,
+                                                    int* s_abort, uint64_t* wait_ticks) {
+  const int lane = lane_id();
+  exchange_publish(a, g, i, s_part);
+  long long S = 0;
+  if (!exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part, &S, s_abort, wait_ticks)) return false;
+  if (lane < g.K) class_targets(g, lane, S + (long long)bias[lane], y_row, s_tgt, s_prob);
   return true;
 }
 
@@ -1075,6 +1121,9 @@ __device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g,
 // per-clause results are those of resident_eval (eval_select with one patch).
 constexpr int kEvalBatch = 4;
 
+// Most D1 passes (of 64 / kn clauses each) that wave 0 takes right after its exchange.
+constexpr int kFusedPasses = 3;
+
 template <bool INJECT>
 __device__ void resident_eval_multi(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int idx0, int stride,
                                     int n_own, const uint32_t* s_planes, const float* s_w, const int* s_drop,
@@ -1137,6 +1186,32 @@ __device__ void resident_eval_multi(const TrainArgs& a, const Geom& g, int j, in
   }
 }
 
+// Fused D1 (train_resident_body): the decisions of sample i were taken while other waves
+// could still be reading the clause's weights for sample i+1, so the task's wave, before its
+// literal updates, takes back the clause's speculative votes of sample i+1 (weights from
+// before the update; spec_sel its selection there, -1 for none) and its patch-weight
+// increment, then stores the new weights staged in task_w.  Lanes < K (coalesced) or lane 0
+// (the own bank's class) take part.
+__device__ __forceinline__ void commit_fused_task(const TrainArgs& a, const Geom& g, int64_t c_begin, int idx,
+                                                  int spec_sel, const float* task_w, float* s_w, long long* part_next,
+                                                  int* s_pw) {
+  const int lane = lane_id();
+  const int64_t c = c_begin + idx;
+  const bool mine = g.coalesced ? lane < g.K : lane == 0;
+  const int64_t k = g.coalesced ? (int64_t)lane : c / g.per_bank;
+  if (mine) {
+    float* wp = s_w + (int64_t)idx * g.K + k;
+    if (spec_sel >= 0) atomicAdd((unsigned long long*)&part_next[k], (unsigned long long)(-(long long)*wp));
+    *wp = task_w[k];
+  }
+  if (lane == 0 && spec_sel >= 0) {
+    if (g.P == 1)
+      s_pw[idx] -= 1;
+    else
+      atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
+  }
+}
+
 // Training with each workgroup's clause state resident in LDS for the whole launch:
 // planes [own][np][W], weights [own][K] (and, with one patch, patch weights [own]) are
 // loaded once, updated in place and written back at the end.  With several patches the
@@ -1158,7 +1233,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   __shared__ int s_tgt[64];
   __shared__ double s_prob[64];
   __shared__ int s_abort;
-  __shared__ int s_ntask, s_nslot;
+  __shared__ int s_ntask[2], s_nslot[2];  // queued tasks / draw slots, by sample parity
   __shared__ unsigned long long s_spec_max;  // profile: slowest wave's time in step 1 (waves >= 1)
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
@@ -1189,7 +1264,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   float* s_uu = s_uq + 3 * cpw * g.K;                             // [3][cpw][K]
   int* s_task_idx = (int*)(s_uu + 3 * cpw * g.K);                 // [cpw]
   int* s_task_sb = s_task_idx + cpw;                              // [cpw] first draw slot
-  int* s_slot_idx = s_task_sb + cpw;                              // [R] clause of a draw slot
+  float* s_task_w = (float*)(s_task_sb + cpw);                    // [cpw][K] new weights (fused D1)
+  int* s_slot_idx = (int*)(s_task_w + cpw * g.K);                 // [R] clause of a draw slot
   int* s_slot_k = s_slot_idx + R;                                 // [R] class of a draw slot
   uint32_t* s_rng = (uint32_t*)(s_slot_k + R);                    // [R][W][kPreGroups][4]
   unsigned long long my_updates = 0ull;
@@ -1215,8 +1291,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   if (threadIdx.x < 128) (&s_part[0][0])[threadIdx.x] = 0;
   if (threadIdx.x == 0) {
     s_abort = 0;
-    s_ntask = 0;
-    s_nslot = 0;
+    s_ntask[0] = s_ntask[1] = 0;
+    s_nslot[0] = s_nslot[1] = 0;
     s_spec_max = 0ull;
   }
   uint64_t spec_ticks = 0;  // profile: this wave's time in step 1 (waves >= 1)
@@ -1252,6 +1328,22 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   }
   __syncthreads();
   prof_last = __builtin_amdgcn_s_memrealtime();
+  // Feedback decisions (D1) take lanes = (clause, class) pairs: kn classes per clause, cpp
+  // clauses per pass of a wave.  When the classes are coalesced and the workgroup's clauses
+  // fit in kFusedPasses passes, wave 0 takes the decisions itself as soon as its exchange
+  // ends ("fused"): every lane polls the total of its own class and derives that class's
+  // feedback, and the other inputs were loaded while the sums were in flight.  The other
+  // waves may still be evaluating sample i+1 then, so the weight changes and the take-back
+  // of speculative votes wait for the task's wave in D3 (commit_fused_task).  Otherwise D1
+  // runs after a barrier, spread over the waves.
+  const int kn = g.coalesced ? (int)g.K : 1;
+  const int cpp = kWave / kn;
+  const int jc = lane / kn, kk = lane - jc * kn;
+  const unsigned long long seg = kn == kWave ? ~0ull : ((1ull << kn) - 1ull);
+  // (from the geometry, which fixes cpw = ceil(C / grid) + 1, so that the specialised
+  // kernels keep only one of the two paths)
+  const int64_t cpw_g = (g.C + g.grid - 1) / g.grid + 1;
+  const bool fused = g.coalesced && (cpw_g + cpp - 1) / cpp <= kFusedPasses;
 
   for (int i = 0; i < a.N; ++i) {
     const uint64_t t = a.step0 + (uint64_t)i;
@@ -1264,11 +1356,82 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     // ---- B + C on wave 0; speculative A of sample i+1 and staging of i+2 on the others
     if (wave == 0) {
       if (lane == 0) {
-        s_ntask = 0;
-        s_nslot = 0;
+        s_ntask[b2] = 0;
+        s_nslot[b2] = 0;
       }
-      exchange_class_sums(a, g, i, s_y + b3 * g.K, s_bias, s_part[b2], s_tgt, s_prob, &s_abort, &wait_ticks);
-      YTM_PROF_MARK(0);
+      if (fused) {
+        exchange_publish(a, g, i, s_part[b2]);
+        // the decisions' inputs, loaded while the class sums are exchanged; lane (jc, kk)
+        // takes class kk of clause p * cpp + jc in pass p
+        const int y_k = s_y[b3 * g.K + kk];
+        const float bias_k = s_bias[kk];
+        float f_w[kFusedPasses], f_uq[kFusedPasses], f_uu[kFusedPasses];
+        int f_sel[kFusedPasses], f_ninc[kFusedPasses];
+        bool f_act[kFusedPasses];
+#pragma unroll
+        for (int p = 0; p < kFusedPasses; ++p) {
+          const int idx = p * cpp + jc;
+          const bool valid = jc < cpp && idx < n_own;
+          const int ix = valid ? idx : 0;  // idle lanes read clause 0 and discard it
+          const int64_t k = kk;
+          f_w[p] = s_w[ix * g.K + k];
+          f_sel[p] = s_sel[b2 * cpw + ix];
+          f_ninc[p] = s_ninc[b2 * cpw + ix];
+          f_act[p] = valid && s_drop[ix] == 0;
+          f_uq[p] = INJECT ? 0.0f : s_uq[((int64_t)b3 * cpw + ix) * g.K + k];
+          f_uu[p] = INJECT ? 0.0f : s_uu[((int64_t)b3 * cpw + ix) * g.K + k];
+        }
+        long long S = 0;
+        const bool ok = exchange_wait(a, g, i, kk, true, s_part[b2], &S, &s_abort, &wait_ticks);
+        YTM_PROF_MARK(0);
+        if (ok) {
+          const ClassFb fb = class_fb(g, S + (long long)bias_k, y_k);  // every lane: class kk
+#pragma unroll
+          for (int p = 0; p < kFusedPasses; ++p) {
+            if (p * cpp >= n_own) continue;  // (no break: the loop must unroll for f_* to stay in registers)
+            const int idx = p * cpp + jc;
+            const bool valid = jc < cpp && idx < n_own;
+            const int ix = valid ? idx : 0;
+            const int64_t c = c_begin + ix;
+            const int64_t k = kk;
+            const PairOps po = decide_pair<INJECT>(g, inj, c, k, f_act[p], f_sel[p], f_ninc[p], fb.tgt, fb.prob, f_w[p],
+                                                   f_uq[p], f_uu[p]);
+            const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
+            if ((b1a | b1b | bt2) == 0ull) continue;
+            const int sh = jc * kn;
+            const unsigned long long m1a = valid ? (b1a >> sh) & seg : 0ull;
+            const unsigned long long m1b = valid ? (b1b >> sh) & seg : 0ull;
+            const unsigned long long m2 = valid ? (bt2 >> sh) & seg : 0ull;
+            const bool changes = (m1a | m1b | m2) != 0ull;
+            const bool leader = changes && kk == 0;
+            my_updates += (unsigned long long)__popcll(__ballot(leader));
+            int tk = 0;
+            if (leader) {
+              const unsigned long long rng = INJECT ? 0ull : (m1a | m1b);
+              tk = atomicAdd(&s_ntask[b2], 1);
+              const int sb = INJECT ? 0 : atomicAdd(&s_nslot[b2], __popcll(rng));
+              s_task_idx[tk] = ix;
+              s_task_sb[tk] = sb;
+              s_task_m[tk * 3 + 0] = m1a;
+              s_task_m[tk * 3 + 1] = m1b;
+              s_task_m[tk * 3 + 2] = m2;
+              int jj = sb;
+              for (unsigned long long r = rng; r; r &= r - 1ull, ++jj) {
+                if (jj < R) {
+                  s_slot_idx[jj] = ix;
+                  s_slot_k[jj] = __ffsll((long long)r) - 1;
+                }
+              }
+            }
+            tk = __shfl(tk, sh);  // the clause's task, from its first lane
+            if (changes) s_task_w[tk * g.K + k] = (po.t1a || po.t2) ? po.w_new : f_w[p];
+          }
+        }
+        YTM_PROF_MARK(2);
+      } else {
+        exchange_class_sums(a, g, i, s_y + b3 * g.K, s_bias, s_part[b2], s_tgt, s_prob, &s_abort, &wait_ticks);
+        YTM_PROF_MARK(0);
+      }
     } else {
       const uint64_t spec_t0 = a.profile ? __builtin_amdgcn_s_memrealtime() : 0;
       // One patch: sample i+2 was read from global memory one iteration ago (one word or
@@ -1318,110 +1481,108 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     // each wave decides its clause (decide, lanes = classes); with more, lanes take
     // (clause, class) pairs, kn classes per clause and 64 / kn clauses per wave pass
     // (decide_pair), and a clause is queued by its first lane.
-    if (n_own <= nwv) {
-      for (int idx = wave; idx < n_own; idx += nwv) {
-        const int64_t c = c_begin + idx;
-        const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
-        const float wold = s_w[idx * g.K + kp];
-        const FbOps ops = decide<INJECT, !INJECT>(a, g, inj, c, t, s_sel[b2 * cpw + idx], s_ninc[b2 * cpw + idx], s_tgt,
-                                                  s_prob, s_w + idx * g.K, s_uq + ((int64_t)b3 * cpw + idx) * g.K,
-                                                  s_uu + ((int64_t)b3 * cpw + idx) * g.K, s_drop[idx] != 0);
-        if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
-        const int spec_sel = more ? s_sel[b2n * cpw + idx] : -1;
-        if (spec_sel >= 0) {
-          if (g.coalesced ? lane < g.K : lane == 0)
-            atomicAdd((unsigned long long*)&s_part[b2n][kp], (unsigned long long)(-(long long)wold));
-          if (lane == 0) {
-            if (g.P == 1)
-              s_pw[idx] -= 1;
-            else
-              atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
-          }
-        }
-        if (lane == 0) {
-          ++my_updates;
-          const unsigned long long rng = INJECT ? 0ull : (ops.m1a | ops.m1b);
-          const int tk = atomicAdd(&s_ntask, 1);
-          const int sb = INJECT ? 0 : atomicAdd(&s_nslot, __popcll(rng));
-          s_task_idx[tk] = idx;
-          s_task_sb[tk] = sb;
-          s_task_m[tk * 3 + 0] = ops.m1a;
-          s_task_m[tk * 3 + 1] = ops.m1b;
-          s_task_m[tk * 3 + 2] = ops.m2;
-          const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
-          int j = sb;
-          for (unsigned long long r = rng; r; r &= r - 1ull, ++j) {
-            if (j < R) {
-              s_slot_idx[j] = idx;
-              s_slot_k[j] = (int)(kb + __ffsll((long long)r) - 1);
-            }
-          }
-        }
-      }
-    } else {
-      const int kn = g.coalesced ? (int)g.K : 1;
-      const int cpp = kWave / kn;  // clauses per pass
-      const int jc = lane / kn, kk = lane - jc * kn;
-      const unsigned long long seg = kn == kWave ? ~0ull : ((1ull << kn) - 1ull);
-      for (int base = wave * cpp; base < n_own; base += nwv * cpp) {
-        const int idx = base + jc;
-        const bool valid = jc < cpp && idx < n_own;
-        const int ix = valid ? idx : base;  // idle lanes read a valid clause and discard it
-        const int64_t c = c_begin + ix;
-        const int64_t k = (g.coalesced ? 0 : c / g.per_bank) + kk;
-        float* wp = s_w + (int64_t)ix * g.K + k;
-        const float wold = *wp;
-        const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && s_drop[ix] == 0, s_sel[b2 * cpw + ix],
-                                               s_ninc[b2 * cpw + ix], s_tgt[k], s_prob[k], wold,
-                                               s_uq[((int64_t)b3 * cpw + ix) * g.K + k],
-                                               s_uu[((int64_t)b3 * cpw + ix) * g.K + k]);
-        if (po.t1a || po.t2) *wp = po.w_new;
-        const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
-        if ((b1a | b1b | bt2) == 0ull) continue;
-        const int sh = jc * kn;
-        const unsigned long long m1a = valid ? (b1a >> sh) & seg : 0ull;
-        const unsigned long long m1b = valid ? (b1b >> sh) & seg : 0ull;
-        const unsigned long long m2 = valid ? (bt2 >> sh) & seg : 0ull;
-        const bool changes = (m1a | m1b | m2) != 0ull;
-        const int spec_sel = more && changes ? s_sel[b2n * cpw + ix] : -1;
-        if (spec_sel >= 0)
-          atomicAdd((unsigned long long*)&s_part[b2n][k], (unsigned long long)(-(long long)wold));
-        const bool leader = changes && kk == 0;
-        my_updates += (unsigned long long)__popcll(__ballot(leader));
-        if (leader) {
+    if (!fused) {
+      if (n_own <= nwv) {
+        for (int idx = wave; idx < n_own; idx += nwv) {
+          const int64_t c = c_begin + idx;
+          const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
+          const float wold = s_w[idx * g.K + kp];
+          const FbOps ops = decide<INJECT, !INJECT>(a, g, inj, c, t, s_sel[b2 * cpw + idx], s_ninc[b2 * cpw + idx], s_tgt,
+                                                    s_prob, s_w + idx * g.K, s_uq + ((int64_t)b3 * cpw + idx) * g.K,
+                                                    s_uu + ((int64_t)b3 * cpw + idx) * g.K, s_drop[idx] != 0);
+          if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
+          const int spec_sel = more ? s_sel[b2n * cpw + idx] : -1;
           if (spec_sel >= 0) {
-            if (g.P == 1)
-              s_pw[ix] -= 1;
-            else
-              atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
+            if (g.coalesced ? lane < g.K : lane == 0)
+              atomicAdd((unsigned long long*)&s_part[b2n][kp], (unsigned long long)(-(long long)wold));
+            if (lane == 0) {
+              if (g.P == 1)
+                s_pw[idx] -= 1;
+              else
+                atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
+            }
           }
-          const unsigned long long rng = INJECT ? 0ull : (m1a | m1b);
-          const int tk = atomicAdd(&s_ntask, 1);
-          const int sb = INJECT ? 0 : atomicAdd(&s_nslot, __popcll(rng));
-          s_task_idx[tk] = ix;
-          s_task_sb[tk] = sb;
-          s_task_m[tk * 3 + 0] = m1a;
-          s_task_m[tk * 3 + 1] = m1b;
-          s_task_m[tk * 3 + 2] = m2;
-          const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
-          int jj = sb;
-          for (unsigned long long r = rng; r; r &= r - 1ull, ++jj) {
-            if (jj < R) {
-              s_slot_idx[jj] = ix;
-              s_slot_k[jj] = (int)(kb + __ffsll((long long)r) - 1);
+          if (lane == 0) {
+            ++my_updates;
+            const unsigned long long rng = INJECT ? 0ull : (ops.m1a | ops.m1b);
+            const int tk = atomicAdd(&s_ntask[b2], 1);
+            const int sb = INJECT ? 0 : atomicAdd(&s_nslot[b2], __popcll(rng));
+            s_task_idx[tk] = idx;
+            s_task_sb[tk] = sb;
+            s_task_m[tk * 3 + 0] = ops.m1a;
+            s_task_m[tk * 3 + 1] = ops.m1b;
+            s_task_m[tk * 3 + 2] = ops.m2;
+            const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+            int j = sb;
+            for (unsigned long long r = rng; r; r &= r - 1ull, ++j) {
+              if (j < R) {
+                s_slot_idx[j] = idx;
+                s_slot_k[j] = (int)(kb + __ffsll((long long)r) - 1);
+              }
+            }
+          }
+        }
+      } else {
+        for (int base = wave * cpp; base < n_own; base += nwv * cpp) {
+          const int idx = base + jc;
+          const bool valid = jc < cpp && idx < n_own;
+          const int ix = valid ? idx : base;  // idle lanes read a valid clause and discard it
+          const int64_t c = c_begin + ix;
+          const int64_t k = (g.coalesced ? 0 : c / g.per_bank) + kk;
+          float* wp = s_w + (int64_t)ix * g.K + k;
+          const float wold = *wp;
+          const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && s_drop[ix] == 0, s_sel[b2 * cpw + ix],
+                                                 s_ninc[b2 * cpw + ix], s_tgt[k], s_prob[k], wold,
+                                                 s_uq[((int64_t)b3 * cpw + ix) * g.K + k],
+                                                 s_uu[((int64_t)b3 * cpw + ix) * g.K + k]);
+          if (po.t1a || po.t2) *wp = po.w_new;
+          const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
+          if ((b1a | b1b | bt2) == 0ull) continue;
+          const int sh = jc * kn;
+          const unsigned long long m1a = valid ? (b1a >> sh) & seg : 0ull;
+          const unsigned long long m1b = valid ? (b1b >> sh) & seg : 0ull;
+          const unsigned long long m2 = valid ? (bt2 >> sh) & seg : 0ull;
+          const bool changes = (m1a | m1b | m2) != 0ull;
+          const int spec_sel = more && changes ? s_sel[b2n * cpw + ix] : -1;
+          if (spec_sel >= 0)
+            atomicAdd((unsigned long long*)&s_part[b2n][k], (unsigned long long)(-(long long)wold));
+          const bool leader = changes && kk == 0;
+          my_updates += (unsigned long long)__popcll(__ballot(leader));
+          if (leader) {
+            if (spec_sel >= 0) {
+              if (g.P == 1)
+                s_pw[ix] -= 1;
+              else
+                atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
+            }
+            const unsigned long long rng = INJECT ? 0ull : (m1a | m1b);
+            const int tk = atomicAdd(&s_ntask[b2], 1);
+            const int sb = INJECT ? 0 : atomicAdd(&s_nslot[b2], __popcll(rng));
+            s_task_idx[tk] = ix;
+            s_task_sb[tk] = sb;
+            s_task_m[tk * 3 + 0] = m1a;
+            s_task_m[tk * 3 + 1] = m1b;
+            s_task_m[tk * 3 + 2] = m2;
+            const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+            int jj = sb;
+            for (unsigned long long r = rng; r; r &= r - 1ull, ++jj) {
+              if (jj < R) {
+                s_slot_idx[jj] = ix;
+                s_slot_k[jj] = (int)(kb + __ffsll((long long)r) - 1);
+              }
             }
           }
         }
       }
+      YTM_PROF_MARK(2);
+      __syncthreads();
+      YTM_PROF_MARK(3);
     }
-    YTM_PROF_MARK(2);
-    __syncthreads();
-    YTM_PROF_MARK(3);
-    const int ntask = s_ntask;
+    const int ntask = s_ntask[b2];
     if (ntask == 0) continue;
     if (!INJECT) {
       // D2: the whole workgroup computes the leading plane groups of every queued draw
-      const int nslot = min(s_nslot, R);
+      const int nslot = min(s_nslot[b2], R);
       const int per_slot = (int)g.W * kPreGroups;
       for (int item = threadIdx.x; item < nslot * per_slot; item += blockDim.x) {
         const int sl = item / per_slot, rem = item % per_slot;
@@ -1445,6 +1606,12 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       // narrow clauses: up to 64 / W tasks per wave at once
       const int per = tasks_per_wave(g, ntask, nwv);
       for (int tk0 = wave * per; tk0 < ntask; tk0 += nwv * per) {
+        if (fused)
+          for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk) {
+            const int idx = s_task_idx[tk];
+            commit_fused_task(a, g, c_begin, idx, more ? s_sel[b2n * cpw + idx] : -1, s_task_w + tk * g.K, s_w,
+                              s_part[b2n], s_pw);
+          }
         apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb,
                             s_sel + b2 * cpw, s_planes, xe, INJECT ? nullptr : s_rng, R);
         if (cap > 0)
@@ -1462,6 +1629,9 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     } else {
       for (int tk = wave; tk < ntask; tk += nwv) {  // tasks round-robin over the waves
         const int idx = s_task_idx[tk];
+        if (fused)
+          commit_fused_task(a, g, c_begin, idx, more ? s_sel[b2n * cpw + idx] : -1, s_task_w + tk * g.K, s_w,
+                            s_part[b2n], s_pw);
         const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
         const int sb = s_task_sb[tk];
         const bool have = !INJECT && sb + __popcll(ops.m1a | ops.m1b) <= R;
