@@ -148,6 +148,41 @@ def test_fit_injected_stream(cfg, n, clauses):
         assert_state_equal(tm, ref, f"epoch {epoch}")
 
 
+@pytest.mark.parametrize("T", [3, 4, 16777215, 16777216])
+def test_update_test_at_its_boundaries(T):
+    """Update draws injected at the probabilities (y - v) / (2y) that clipped class sums
+    v in [-T, T] give (kernel.cu:508-529), rounded to float, and at the floats either side.
+    The GPU's feedback decisions for a few clauses per workgroup test u <= prob without
+    the division, and clip the integer sum, for integral T < 2^24; 2^24 takes the division.
+    The oracle divides (double, IEEE), so every equality and rounding case is checked."""
+    kw = dict(number_of_clauses_per_class=8, T=T, s=3.0, dim=(16, 1, 1), n_classes=3, seed=11)
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(8, T, 3.0, (16, 1, 1), 3, seed=11)
+    n = 60
+    rng = np.random.default_rng(T % 1009)
+    X = (rng.random((n, 16)) < 0.5).astype(np.uint32)
+    y = rng.integers(0, 3, size=n).astype(np.uint32)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    C, K, P, L = tm.number_of_clauses, 3, tm.number_of_patches, tm.number_of_literals
+    vs = np.arange(-min(T, 40), min(T, 40) + 1, dtype=np.float64)
+    vs = np.concatenate([vs, [-T, T]])
+    q = np.concatenate([(T - vs) / (2.0 * T), (-T - vs) / (-2.0 * T)])
+    f = q.astype(np.float32)
+    cand = np.unique(np.concatenate([f, np.nextafter(f, np.float32(2)), np.nextafter(f, np.float32(-1))]))
+    cand = cand[(cand > 0) & (cand <= 1)]
+    block = C * P + 2 * C * K + C * K * L
+    lo, hi = C * P + C * K, C * P + 2 * C * K  # the update draws of a sample block
+    for epoch in range(3):
+        inj = rng.random(tm.random_stream_size(n)).astype(np.float32).reshape(n, block)
+        inj[:, lo:hi] = rng.choice(cand, size=(n, hi - lo))
+        inj = inj.ravel()
+        tm.fit(encX, y, is_X_encoded=True, random_stream=inj)
+        upd = ref.fit_encoded(encX, encY, inject=inj)
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"T={T} epoch {epoch}")
+
+
 @pytest.mark.parametrize(
     "opts",
     [pytest.param(dict(coalesced=False), marks=pytest.mark.skip(reason=BANKS_OFF)),

@@ -495,34 +495,63 @@ __device__ FbOps decide(const TrainArgs& a, const Geom& g, const float* inj, int
 
 // The decision of decide() for one (clause, class) pair held by the calling lane (its own
 // clause c and class k), with the pre-drawn Q-skip and update draws uq, uu (or the
-// injected ones).  Not wave-uniform: every lane may hold another clause.
+// injected ones).  The update test (double)uu <= prob is made as (double)uu * den <= num:
+// den = 1, num = prob, or the exact division-free form of class_fb_exact.  Not
+// wave-uniform: every lane may hold another clause.
 struct PairOps {
   bool t1a, t1b, t2;
   float w_new;
 };
 
+// What a pair's decision needs besides its class's target and the update test's right-hand
+// side: everything that is known before the class sums are (pair_pre), so that only
+// pair_decide is left once they arrive.
+struct PairPre {
+  int flags;  // bit 0 act, 1 o (selected), 2 small (o and ninc <= MAXINC), 3 qskip, 4 w0 < 0, 5 w0 >= 0
+  double ud;  // (double)uu * den
+  float w0;
+};
+
 template <bool INJECT>
-__device__ __forceinline__ PairOps decide_pair(const Geom& g, const float* inj, int64_t c, int64_t k, bool act, int sel,
-                                               int ninc, int tgt, double prob, float w0, float uq, float uu) {
+__device__ __forceinline__ PairPre pair_pre(const Geom& g, const float* inj, int64_t c, int64_t k, bool act, int sel,
+                                            int ninc, double den, float w0, float uq, float uu) {
   if (INJECT) {
     uq = inj[g.C * g.P + c * g.K + k];
     uu = inj[g.C * g.P + g.C * g.K + c * g.K + k];
   }
   const bool o = sel >= 0;
-  const bool small = o && ninc <= g.maxinc;
-  const bool skip = tgt == -1 && (double)uq > g.q_prob;
-  const int sign = (w0 >= 0.0f) - (w0 < 0.0f);
-  const bool upd = act && !skip && (double)uu <= prob;
+  PairPre r;
+  r.flags = (int)act | (int)o << 1 | (int)(o && ninc <= g.maxinc) << 2 | (int)((double)uq > g.q_prob) << 3 |
+            (int)(w0 < 0.0f) << 4 | (int)(w0 >= 0.0f) << 5;
+  r.ud = (double)uu * den;
+  r.w0 = w0;
+  return r;
+}
+
+// Keeps a PairPre computed where it stands (ahead of a wait) instead of where it is used.
+__device__ __forceinline__ void pin(PairPre& q) { asm volatile("" : "+v"(q.flags), "+v"(q.ud), "+v"(q.w0)); }
+
+__device__ __forceinline__ PairOps pair_decide(const Geom& g, const PairPre& q, int tgt, double num) {
+  const bool act = q.flags & 1, o = (q.flags >> 1) & 1, small = (q.flags >> 2) & 1, qskip = (q.flags >> 3) & 1;
+  const int sign = ((q.flags >> 5) & 1) - ((q.flags >> 4) & 1);  // (w0 >= 0) - (w0 < 0)
+  const bool skip = tgt == -1 && qskip;
+  const bool upd = act && !skip && q.ud <= num;
   const int ts = tgt * sign;
   PairOps r;
   r.t1a = upd && ts > 0 && small;
   r.t1b = upd && ts > 0 && !small;
   r.t2 = upd && ts < 0 && o;
-  const float wa = w0 + (float)sign * 1.0f;
-  float wb = w0 - (float)sign * 1.0f;
+  const float wa = q.w0 + (float)sign * 1.0f;
+  float wb = q.w0 - (float)sign * 1.0f;
   if (!g.negative_polarity) wb = wb < 1.0f ? 1.0f : wb;
   r.w_new = r.t1a ? wa : wb;
   return r;
+}
+
+template <bool INJECT>
+__device__ __forceinline__ PairOps decide_pair(const Geom& g, const float* inj, int64_t c, int64_t k, bool act, int sel,
+                                               int ninc, int tgt, double num, double den, float w0, float uq, float uu) {
+  return pair_decide(g, pair_pre<INJECT>(g, inj, c, k, act, sel, ninc, den, w0, uq, uu), tgt, num);
 }
 
 // Literal updates of one clause for the feedback decided in ops, applied class by class
@@ -668,6 +697,43 @@ __device__ __forceinline__ ClassFb class_fb(const Geom& g, long long S, int y) {
   const float cs = (float)S;
   const float vclip = ((double)cs > g.thresh) ? (float)g.thresh : (((double)cs < -g.thresh) ? (float)(-g.thresh) : cs);
   return ClassFb{1 - 2 * (vclip > (float)y), ((double)y - (double)vclip) / (2.0 * (double)y)};
+}
+
+// class_fb without the int64 -> float conversion and the division, for an integral
+// threshold 0 <= T < 2^24 and a target 0 < |y| < 2^28 (exact).  The clip is taken on the
+// integer sum: for such T, (float)S > T exactly when S > T, and |S| <= T converts exactly,
+// so clip((float)S) == (float)clip(S).  The update test (double)u <= prob with
+// prob = RN((y - v) / (2y)) becomes u * |2y| <= (y - v) * sign(y), all terms exact in
+// double: for a float u = m * 2^e (m < 2^24, |u| < 2^24) and q = (y - v) / (2y), q != u
+// implies |q - u| >= 2^min(e, 0) / |2y| > half an ulp of u, so rounding q cannot cross u,
+// and RN(q) >= u exactly when q >= u.  class_prep takes what depends on y only (ahead of
+// the exchange); class_test returns {tgt, num, den} for decide_pair.
+struct ClassPrep {
+  int y;
+  bool exact;
+  double den;  // |2y| (exact) or 1
+};
+
+struct ClassTest {
+  int tgt;
+  double num, den;
+};
+
+__device__ __forceinline__ ClassPrep class_prep(const Geom& g, int y) {
+  const bool tok = g.thresh >= 0.0 && g.thresh < 16777216.0 && g.thresh == (double)(int)g.thresh;
+  const bool exact = tok && y != 0 && y > -(1 << 28) && y < (1 << 28);
+  return ClassPrep{y, exact, exact ? (double)(y > 0 ? 2 * y : -2 * y) : 1.0};
+}
+
+__device__ __forceinline__ ClassTest class_test(const Geom& g, long long S, const ClassPrep& cp) {
+  if (cp.exact) {
+    const int T = (int)g.thresh;
+    int v = S > (long long)T ? T : (S < -(long long)T ? -T : (int)S);
+    asm volatile("" : "+v"(v));  // v is a 32-bit value from here on: one-instruction conversions
+    return ClassTest{1 - 2 * ((float)v > (float)cp.y), (double)(cp.y > 0 ? cp.y - v : v - cp.y), cp.den};
+  }
+  const ClassFb r = class_fb(g, S, cp.y);
+  return ClassTest{r.tgt, r.prob, 1.0};
 }
 
 // class_fb of class k, stored to s_tgt[k] / s_prob[k].
@@ -1344,6 +1410,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   // kernels keep only one of the two paths)
   const int64_t cpw_g = (g.C + g.grid - 1) / g.grid + 1;
   const bool fused = g.coalesced && (cpw_g + cpp - 1) / cpp <= kFusedPasses;
+  const long long bias_kk = (long long)s_bias[kk < g.K ? kk : 0];  // fused: class kk's bias (fixed for the launch)
 
   for (int i = 0; i < a.N; ++i) {
     const uint64_t t = a.step0 + (uint64_t)i;
@@ -1363,41 +1430,35 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         exchange_publish(a, g, i, s_part[b2]);
         // the decisions' inputs, loaded while the class sums are exchanged; lane (jc, kk)
         // takes class kk of clause p * cpp + jc in pass p
-        const int y_k = s_y[b3 * g.K + kk];
-        const float bias_k = s_bias[kk];
-        float f_w[kFusedPasses], f_uq[kFusedPasses], f_uu[kFusedPasses];
-        int f_sel[kFusedPasses], f_ninc[kFusedPasses];
-        bool f_act[kFusedPasses];
+        const ClassPrep cp = class_prep(g, s_y[b3 * g.K + kk]);
+        PairPre pre[kFusedPasses];
 #pragma unroll
         for (int p = 0; p < kFusedPasses; ++p) {
           const int idx = p * cpp + jc;
           const bool valid = jc < cpp && idx < n_own;
           const int ix = valid ? idx : 0;  // idle lanes read clause 0 and discard it
           const int64_t k = kk;
-          f_w[p] = s_w[ix * g.K + k];
-          f_sel[p] = s_sel[b2 * cpw + ix];
-          f_ninc[p] = s_ninc[b2 * cpw + ix];
-          f_act[p] = valid && s_drop[ix] == 0;
-          f_uq[p] = INJECT ? 0.0f : s_uq[((int64_t)b3 * cpw + ix) * g.K + k];
-          f_uu[p] = INJECT ? 0.0f : s_uu[((int64_t)b3 * cpw + ix) * g.K + k];
+          pre[p] = pair_pre<INJECT>(g, inj, c_begin + ix, k, valid && s_drop[ix] == 0, s_sel[b2 * cpw + ix],
+                                    s_ninc[b2 * cpw + ix], cp.den, s_w[ix * g.K + k],
+                                    INJECT ? 0.0f : s_uq[((int64_t)b3 * cpw + ix) * g.K + k],
+                                    INJECT ? 0.0f : s_uu[((int64_t)b3 * cpw + ix) * g.K + k]);
+          pin(pre[p]);
         }
         long long S = 0;
         const bool ok = exchange_wait(a, g, i, kk, true, s_part[b2], &S, &s_abort, &wait_ticks);
         YTM_PROF_MARK(0);
         if (ok) {
-          const ClassFb fb = class_fb(g, S + (long long)bias_k, y_k);  // every lane: class kk
+          const ClassTest fb = class_test(g, S + bias_kk, cp);  // every lane: class kk
 #pragma unroll
           for (int p = 0; p < kFusedPasses; ++p) {
-            if (p * cpp >= n_own) continue;  // (no break: the loop must unroll for f_* to stay in registers)
+            if (p * cpp >= n_own) continue;  // (no break: the loop must unroll for pre[] to stay in registers)
+            const PairOps po = pair_decide(g, pre[p], fb.tgt, fb.num);
+            const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
+            if ((b1a | b1b | bt2) == 0ull) continue;
             const int idx = p * cpp + jc;
             const bool valid = jc < cpp && idx < n_own;
             const int ix = valid ? idx : 0;
-            const int64_t c = c_begin + ix;
             const int64_t k = kk;
-            const PairOps po = decide_pair<INJECT>(g, inj, c, k, f_act[p], f_sel[p], f_ninc[p], fb.tgt, fb.prob, f_w[p],
-                                                   f_uq[p], f_uu[p]);
-            const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
-            if ((b1a | b1b | bt2) == 0ull) continue;
             const int sh = jc * kn;
             const unsigned long long m1a = valid ? (b1a >> sh) & seg : 0ull;
             const unsigned long long m1b = valid ? (b1b >> sh) & seg : 0ull;
@@ -1424,7 +1485,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
               }
             }
             tk = __shfl(tk, sh);  // the clause's task, from its first lane
-            if (changes) s_task_w[tk * g.K + k] = (po.t1a || po.t2) ? po.w_new : f_w[p];
+            if (changes) s_task_w[tk * g.K + k] = (po.t1a || po.t2) ? po.w_new : pre[p].w0;
           }
         }
         YTM_PROF_MARK(2);
@@ -1532,7 +1593,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
           float* wp = s_w + (int64_t)ix * g.K + k;
           const float wold = *wp;
           const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && s_drop[ix] == 0, s_sel[b2 * cpw + ix],
-                                                 s_ninc[b2 * cpw + ix], s_tgt[k], s_prob[k], wold,
+                                                 s_ninc[b2 * cpw + ix], s_tgt[k], s_prob[k], 1.0, wold,
                                                  s_uq[((int64_t)b3 * cpw + ix) * g.K + k],
                                                  s_uu[((int64_t)b3 * cpw + ix) * g.K + k]);
           if (po.t1a || po.t2) *wp = po.w_new;
