@@ -56,15 +56,19 @@ __device__ __forceinline__ uint32_t literal_draw_mask(const TrainArgs& a, const 
     if (g.s_thr >= (1u << 24)) return need;
     if (g.s_thr == 0u) return 0u;
     uint32_t lt = 0u, eq = need;
-    for (int grp = 0; grp < 6; ++grp) {
-      if (!__any(eq != 0u)) break;
-      U4 z;
-      if (have_pre && grp < kPreGroups) {
-        // plane group computed ahead of time by the workgroup (zero words for idle lanes)
-        z = pre ? U4{pre[grp * 4 + 0], pre[grp * 4 + 1], pre[grp * 4 + 2], pre[grp * 4 + 3]} : U4{0u, 0u, 0u, 0u};
-      } else {
-        z = site_words(a.seed, t, (uint32_t)c, TAG_LIT, (uint32_t)((k * g.W + w) * 6 + grp));
+    bool done = false;
+#pragma unroll
+    for (int grp = 0; grp < 6; ++grp) {  // unrolled (no break), which schedules the Philox rounds better
+      if (done) continue;
+      if (!__any(eq != 0u)) {
+        done = true;
+        continue;
       }
+      // a plane group computed ahead of time by the workgroup (zero words for idle lanes)
+      const U4 z = (have_pre && grp < kPreGroups)
+                       ? (pre ? U4{pre[grp * 4 + 0], pre[grp * 4 + 1], pre[grp * 4 + 2], pre[grp * 4 + 3]}
+                              : U4{0u, 0u, 0u, 0u})
+                       : site_words(a.seed, t, (uint32_t)c, TAG_LIT, (uint32_t)((k * g.W + w) * 6 + grp));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = 23 - 4 * grp - i;
@@ -160,6 +164,29 @@ __device__ __forceinline__ uint32_t all_patches_word(const Geom& g) {
 // counts, then its bit by a select.  Wave-uniform.
 __device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* list, int cap) {
   const int lane = lane_id();
+  if (g.W <= kWave) {
+    // one word per lane: lane w writes its word's included literals from its prefix offset,
+    // lowest bit first, so the list is in increasing literal order as below
+    uint32_t mv = lane < g.W ? m[lane] : 0u;
+    const int pc = __popc(mv);
+    const int incl = wave_inclusive_scan(pc);
+    const int total = lane_value(incl, kWave - 1);
+    int pos = incl - pc;
+    const unsigned long long nz = __ballot(mv != 0u);
+    const int hi = nz ? 63 - __clzll((long long)nz) : 0;  // lane of the last included literal
+    const int last = lane_value(32 * lane + 31 - __clz((int)(mv | 1u)), hi);
+    while (mv) {
+      const int b = __ffs((int)mv) - 1;
+      if (pos < cap) list[pos] = (uint16_t)(32 * lane + b);
+      ++pos;
+      mv &= mv - 1u;
+    }
+    if (total > 0 && total <= cap) {
+      const int pad_end = ((total + 7) & ~7) < cap ? ((total + 7) & ~7) : cap;
+      for (int p = total + lane; p < pad_end; p += kWave) list[p] = (uint16_t)last;
+    }
+    return total;
+  }
   int total = 0, last = 0;
   for (int64_t wb = 0; wb < g.W; wb += kWave) {
     const uint32_t mv = wb + lane < g.W ? m[wb + lane] : 0u;
