@@ -416,12 +416,7 @@ __global__ __launch_bounds__(256) void score_lm_kernel(const uint32_t* __restric
     const int64_t e = blk / nch, ch = blk % nch;
     const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
     __syncthreads();  // the previous sample is no longer read
-    const uint32_t* src = XT + e * xtw;
-    if ((xtw & 1) == 0) {
-      for (int64_t j = threadIdx.x; j < xtw / 2; j += blockDim.x) ((uint2*)s_xts)[j] = ((const uint2*)src)[j];
-    } else {
-      for (int64_t j = threadIdx.x; j < xtw; j += blockDim.x) s_xts[j] = src[j];
-    }
+    copy_to_lds(s_xts, XT + e * xtw, xtw, threadIdx.x, blockDim.x);
     __syncthreads();
     long long sum = 0;
     for (int64_t c = c0 + wave; c < c1; c += nwv) {
@@ -470,6 +465,7 @@ __global__ __launch_bounds__(256) void score_finish_kernel(const long long* __re
 // each output row is written coalesced.  MAXQ bounds W by 4*MAXQ words.
 constexpr int kTileC = 96;
 constexpr int kTileMaxK = 16;
+constexpr int kTileStage = 8;  // staged words in flight per thread
 
 template <int MAXQ, int MODE, bool SUM32>
 __global__ __launch_bounds__(256) void tile_kernel(const uint32_t* __restrict__ planes,
@@ -491,17 +487,42 @@ __global__ __launch_bounds__(256) void tile_kernel(const uint32_t* __restrict__ 
     const int64_t e0 = (blk / nch) * 256 + wave * kWave, c0 = (blk % nch) * kTileC;
     const int nc = (int)(c0 + kTileC < g.C ? kTileC : g.C - c0);
     __syncthreads();  // the previous chunk is no longer read
-    for (int j = threadIdx.x; j < nc * 4 * MAXQ; j += blockDim.x) {
-      const int cl = j / (4 * MAXQ), ww = j % (4 * MAXQ);
-      ((uint32_t*)s_m)[j] = ww < g.W ? planes[((c0 + cl) * g.np + g.np - 1) * g.W + ww] : 0u;
+    // Staging: every load reads a valid address (clamped) and is issued before any of the
+    // batch is used, so a thread's loads overlap instead of waiting one by one.
+    for (int j0 = threadIdx.x; j0 < nc * 4 * MAXQ; j0 += kTileStage * blockDim.x) {
+      uint32_t v[kTileStage];
+#pragma unroll
+      for (int b = 0; b < kTileStage; ++b) {
+        const int j = j0 + b * blockDim.x;
+        const int cl = j / (4 * MAXQ), ww = j % (4 * MAXQ);
+        const bool ok = j < nc * 4 * MAXQ && ww < g.W;
+        v[b] = planes[ok ? ((c0 + cl) * g.np + g.np - 1) * g.W + ww : 0];
+        v[b] = ok ? v[b] : 0u;
+      }
+#pragma unroll
+      for (int b = 0; b < kTileStage; ++b)
+        if (j0 + b * (int)blockDim.x < nc * 4 * MAXQ) ((uint32_t*)s_m)[j0 + b * blockDim.x] = v[b];
     }
     for (int j = threadIdx.x; j < nc; j += blockDim.x) s_live[j] = ninc[c0 + j] != 0;
     if (MODE == 0)
-      for (int j = threadIdx.x; j < nc * (int)g.K; j += blockDim.x) s_w[j] = (Sum)w[c0 * g.K + j];
+      for (int j0 = threadIdx.x; j0 < nc * (int)g.K; j0 += kTileStage * blockDim.x) {
+        float v[kTileStage];
+#pragma unroll
+        for (int b = 0; b < kTileStage; ++b) {
+          const int j = j0 + b * blockDim.x;
+          v[b] = w[c0 * g.K + (j < nc * (int)g.K ? j : 0)];
+        }
+#pragma unroll
+        for (int b = 0; b < kTileStage; ++b)
+          if (j0 + b * (int)blockDim.x < nc * (int)g.K) s_w[j0 + b * blockDim.x] = (Sum)v[b];
+      }
     const int64_t e = e0 + lane;
+    const uint32_t* xr = X + (e < N ? e : N - 1) * g.W;  // lanes past N read the last sample and discard it
     uint32_t nx[4 * MAXQ];
 #pragma unroll
-    for (int ww = 0; ww < 4 * MAXQ; ++ww) nx[ww] = (ww < g.W && e < N) ? ~X[e * g.W + ww] : 0u;
+    for (int ww = 0; ww < 4 * MAXQ; ++ww) nx[ww] = xr[ww < g.W ? ww : 0];
+#pragma unroll
+    for (int ww = 0; ww < 4 * MAXQ; ++ww) nx[ww] = (ww < g.W && e < N) ? ~nx[ww] : 0u;
     Sum sum[MODE == 0 ? kTileMaxK : 1];
 #pragma unroll
     for (int k = 0; k < (MODE == 0 ? kTileMaxK : 1); ++k) sum[k] = 0;
@@ -583,8 +604,7 @@ __global__ __launch_bounds__(256) void transform_lm_kernel(const uint32_t* __res
     const int64_t e = blk / nch, ch = blk % nch;
     const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
     __syncthreads();  // the previous sample is no longer read
-    const uint32_t* src = XT + e * xtw;
-    for (int64_t j = threadIdx.x; j < xtw; j += blockDim.x) s_xts[j] = src[j];
+    copy_to_lds(s_xts, XT + e * xtw, xtw, threadIdx.x, blockDim.x);
     __syncthreads();
     for (int64_t c = c0 + wave; c < c1; c += nwv) {
       const int n = nlit[c];

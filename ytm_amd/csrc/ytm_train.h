@@ -920,9 +920,9 @@ __device__ __forceinline__ void copy_to_lds(uint32_t* dst, const uint32_t* src, 
     for (int64_t j0 = first; j0 < n2; j0 += (int64_t)count * kCopyBatch) {
       uint2 v[kCopyBatch];
 #pragma unroll
-      for (int b = 0; b < kCopyBatch; ++b) {
+      for (int b = 0; b < kCopyBatch; ++b) {  // unconditional (clamped) loads, all in flight together
         const int64_t j = j0 + (int64_t)b * count;
-        if (j < n2) v[b] = s2[j];
+        v[b] = s2[j < n2 ? j : n2 - 1];
       }
 #pragma unroll
       for (int b = 0; b < kCopyBatch; ++b) {
@@ -936,7 +936,7 @@ __device__ __forceinline__ void copy_to_lds(uint32_t* dst, const uint32_t* src, 
 #pragma unroll
       for (int b = 0; b < kCopyBatch; ++b) {
         const int64_t j = j0 + (int64_t)b * count;
-        if (j < n) v[b] = src[j];
+        v[b] = src[j < n ? j : n - 1];
       }
 #pragma unroll
       for (int b = 0; b < kCopyBatch; ++b) {
