@@ -369,6 +369,28 @@ def test_score_edge_cases():
     np.testing.assert_array_equal(tm.score(encXt[:7], is_X_encoded=True), ref.score(encXt[:7]))
 
 
+def test_one_patch_edge_batches():
+    """One patch (the sample-tiled kernels, 64 samples per wave, 256 per block): an empty fit,
+    a one-sample fit, and scores / clause outputs for batch sizes on either side of the tile
+    edges, where the lanes past the last sample read a clamped sample and discard it."""
+    tm, ref, X, y, Xt, yt = pair(2, 40, 300, clauses=30)
+    encX, encXt = tm.encode(X), tm.encode(Xt)
+    empty = np.zeros((0,) + encX.shape[1:], dtype=np.uint32)
+    tm.fit(empty, np.zeros(0, dtype=np.uint32), is_X_encoded=True)
+    assert tm.stats()["last_fit_samples"] == 0
+    assert_state_equal(tm, ref, "after an empty fit")
+    tm.fit(encX[:1], y[:1], is_X_encoded=True)
+    ref.fit_encoded(encX[:1], ref.encode_y_multiclass(y[:1]))
+    tm.fit(encX, y, is_X_encoded=True)
+    ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+    assert_state_equal(tm, ref, "after one sample and one epoch")
+    assert tm.score(empty, is_X_encoded=True).shape == (0, 10)
+    for n in (1, 63, 65, 255, 257, 300):
+        np.testing.assert_array_equal(tm.score(encXt[:n], is_X_encoded=True), ref.score(encXt[:n]), err_msg=f"n={n}")
+        np.testing.assert_array_equal(tm.transform(encXt[:n], is_X_encoded=True), ref.transform(encXt[:n]),
+                                      err_msg=f"n={n}")
+
+
 # ------------------------------------------------------------------ API surface
 def test_api_shapes_dtypes_errors():
     tm, *_ = pair(3, 4, clauses=50)
