@@ -33,6 +33,15 @@ constexpr uint64_t kWaitTicks = 200000000ull;
 // resident kernel computes cooperatively ahead of applying an update.
 constexpr int kPreGroups = 3;
 
+// Plane groups that decide u <= S_INV, i.e. q < s_thr for the 24-bit integer q of a literal
+// draw, taken most significant plane first.  Below the lowest set bit of s_thr nothing more
+// can make q < s_thr: a literal still equal to s_thr on the planes above it is decided
+// "not less", so only the groups down to that bit matter (one group for s_thr = 2^23,
+// S_INV = 0.5).  None for s_thr = 0 or >= 2^24, which are decided without draws.
+__device__ __forceinline__ int draw_groups(uint32_t s_thr) {
+  return (s_thr == 0u || s_thr >= (1u << 24)) ? 0 : (23 - __builtin_ctz(s_thr)) / 4 + 1;
+}
+
 __device__ __forceinline__ int wave_inclusive_scan(int v) { return wave_scan_add_i32(v); }
 
 // Literal-decrement mask of one (clause, class) update for the 32 literals of word w:
@@ -57,9 +66,10 @@ __device__ __forceinline__ uint32_t literal_draw_mask(const TrainArgs& a, const 
     if (g.s_thr == 0u) return 0u;
     uint32_t lt = 0u, eq = need;
     bool done = false;
+    const int ngrp = draw_groups(g.s_thr);
 #pragma unroll
     for (int grp = 0; grp < 6; ++grp) {  // unrolled (no break), which schedules the Philox rounds better
-      if (done) continue;
+      if (done || grp >= ngrp) continue;
       if (!__any(eq != 0u)) {
         done = true;
         continue;
@@ -1671,11 +1681,12 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     if (!INJECT) {
       // D2: the whole workgroup computes the leading plane groups of every queued draw
       const int nslot = min(s_nslot[b2], R);
-      const int per_slot = (int)g.W * kPreGroups;
-      for (int item = threadIdx.x; item < nslot * per_slot; item += blockDim.x) {
+      const int npre = draw_groups(g.s_thr) < kPreGroups ? draw_groups(g.s_thr) : kPreGroups;
+      const int per_slot = (int)g.W * npre;
+      for (int item = threadIdx.x; npre > 0 && item < nslot * per_slot; item += blockDim.x) {
         const int sl = item / per_slot, rem = item % per_slot;
-        const int64_t w = rem / kPreGroups;
-        const int grp = rem % kPreGroups;
+        const int64_t w = rem / npre;
+        const int grp = rem % npre;
         const int64_t k = s_slot_k[sl];
         const U4 z = site_words(a.seed, t, (uint32_t)(c_begin + s_slot_idx[sl]), TAG_LIT,
                                 (uint32_t)((k * g.W + w) * 6 + grp));
