@@ -572,8 +572,10 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (N == 0) return YTM_OK;
   long long* acc = nullptr;
   float* dout = nullptr;
-  void* lists = nullptr;  // several patches: the clauses' literal lists
-  const size_t lists_bytes = ds->d_XT ? ytm::score_lists_bytes(g) : 0;
+  void* lists = nullptr;  // several patches, or one patch with wide clauses: the literal lists
+  const size_t lm_bytes = ds->d_XT ? ytm::score_lists_bytes(g) : 0;
+  const size_t wide_bytes = lm_bytes ? 0 : ytm::score_wide_bytes(g);
+  const size_t lists_bytes = lm_bytes ? lm_bytes : wide_bytes;
   const int64_t chunks = lists_bytes ? 0 : ytm::score_tile_chunks(g);  // one patch: per-chunk sums
   HIP_TRY(hipMalloc(&acc, (size_t)(N * g.K * (chunks ? chunks : 1)) * 8));
   hipError_t e = hipMalloc(&dout, (size_t)(N * g.K) * 4);
@@ -583,7 +585,9 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (e == hipSuccess && !chunks) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
   if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
   if (e == hipSuccess) {
-    if (lists)
+    if (wide_bytes)
+      e = ytm::launch_score_wide(m->d_planes, m->d_w, ds->d_X, N, g, lists, acc, m->stream);
+    else if (lists)
       e = ytm::launch_score_lm(m->d_planes, m->d_w, ds->d_XT, N, g, lists, acc, m->stream);
     else if (chunks)
       e = ytm::launch_score_tile(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->w_bound, m->stream);

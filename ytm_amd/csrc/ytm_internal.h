@@ -36,6 +36,13 @@ hipError_t launch_score_parts_finish(const long long* parts, int64_t nch, const 
 size_t score_lists_bytes(const Geom& g);
 hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_t* XT, int64_t N, const Geom& g,
                            void* scratch, long long* acc, hipStream_t s);
+// One patch and clauses wider than 64 words: a tile of samples transposed in LDS, the
+// clauses' literal lists AND-ed lane by lane; scratch holds score_wide_bytes(g); acc (zeroed
+// first) receives each sample's exact sums.
+bool score_wide_fits(const Geom& g);
+size_t score_wide_bytes(const Geom& g);  // 0 when score_wide_fits is false
+hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint32_t* X, int64_t N, const Geom& g,
+                             void* scratch, long long* acc, hipStream_t s);
 hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t N, const Geom& g,
                                float* out, hipStream_t s);
 // Clause outputs; mode 0: any patch (N, C); 1: per patch (N, C, P); 2: per patch, bit-packed

@@ -740,6 +740,101 @@ hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s) {
   return hipGetLastError();
 }
 
+// One patch, clauses wider than the sample tiles take (W > 64): a block takes kWideTile
+// samples and every clause.  The samples are transposed in LDS into one word per literal
+// (bit s: the literal is 1 in sample e0 + s), 32 ballots per pair of sample words.  A lane
+// takes a clause and ANDs the words of its included literals, 8 per step from its literal
+// list, stopping once no sample of the tile is left; the tile's samples that the clause
+// fires on get its weights in LDS int64 sums (calc_class_sums_infer_batch, kernel.cu:319-343:
+// empty clauses do not vote).  Clauses with more literals than the list holds are AND-ed
+// by the whole wave from their include masks.  With few tiles the clauses are split into
+// nch chunks over blocks; each block adds its chunk's exact sums into acc[e][k] (zeroed
+// before the launch).
+constexpr int kWideTile = 32;
+constexpr int64_t kWideLdsBytes = 96 * 1024;
+
+__global__ __launch_bounds__(1024) void score_wide_kernel(const uint32_t* __restrict__ planes,
+                                                          const uint16_t* __restrict__ lists,
+                                                          const int32_t* __restrict__ nlit,
+                                                          const float* __restrict__ w,
+                                                          const uint32_t* __restrict__ X, int64_t N, Geom g,
+                                                          int64_t nch, long long* __restrict__ acc) {
+  extern __shared__ uint32_t s_xw[];  // [W * 32]: word l = literal l over the tile's samples
+  __shared__ long long s_sum[kWideTile * kTileMaxK];
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave, nwv = blockDim.x / kWave;
+  const int sl = lane & 31, half = lane >> 5;  // transpose: sample sl of word 2 * pair + half
+  const int64_t ntile = (N + kWideTile - 1) / kWideTile;
+  const int64_t csz = ((g.C + nch - 1) / nch + kWave - 1) / kWave * kWave;  // clauses per chunk, whole waves
+  for (int64_t blk = blockIdx.x; blk < ntile * nch; blk += gridDim.x) {
+    const int64_t tile = blk / nch, cb = (blk % nch) * csz;
+    const int64_t ce = cb + csz < g.C ? cb + csz : g.C;
+    const int64_t e0 = tile * kWideTile;
+    const int ns = (int)(N - e0 < kWideTile ? N - e0 : kWideTile);
+    __syncthreads();  // the previous tile is no longer read
+    for (int j = threadIdx.x; j < kWideTile * (int)g.K; j += blockDim.x) s_sum[j] = 0;
+    for (int64_t pair = wave; pair < (g.W + 1) / 2; pair += nwv) {
+      const int64_t wd = 2 * pair + half;
+      const bool ok = wd < g.W && sl < ns;
+      const uint32_t xr = X[(e0 + (sl < ns ? sl : 0)) * g.W + (wd < g.W ? wd : 0)];  // clamped, unconditional
+      const uint32_t x = ok ? xr : 0u;
+      uint32_t mine = 0u;
+#pragma unroll
+      for (int b = 0; b < 32; ++b) {
+        const unsigned long long bal = __ballot((x >> b) & 1u);
+        const uint32_t part = half ? (uint32_t)(bal >> 32) : (uint32_t)bal;
+        mine = sl == b ? part : mine;
+      }
+      if (wd < g.W) s_xw[wd * 32 + sl] = mine;  // literal 32 * wd + sl
+    }
+    __syncthreads();
+    const uint32_t live = ns == 32 ? 0xFFFFFFFFu : ((1u << ns) - 1u);
+    const int np = g.np;
+    for (int64_t c0 = cb + (int64_t)wave * kWave; c0 < ce; c0 += (int64_t)nwv * kWave) {
+      const int64_t c = c0 + lane;
+      const int n = c < ce ? nlit[c] : 0;
+      uint32_t fire = 0u;
+      if (n > 0 && n <= kScoreListCap) {
+        fire = live;
+        const uint16_t* lst = lists + c * kScoreListCap;
+        for (int j = 0; j < n && fire; j += 8) {  // the list is padded to a multiple of 8
+          const uint4 q = *(const uint4*)(lst + j);
+          fire &= s_xw[q.x & 0xFFFFu] & s_xw[q.x >> 16] & s_xw[q.y & 0xFFFFu] & s_xw[q.y >> 16] &
+                  s_xw[q.z & 0xFFFFu] & s_xw[q.z >> 16] & s_xw[q.w & 0xFFFFu] & s_xw[q.w >> 16];
+        }
+      }
+      if (fire) {
+        for (int k = 0; k < (int)g.K; ++k) {
+          const long long v = (long long)w[c * g.K + k];
+          for (uint32_t f = fire; f; f &= f - 1u)
+            atomicAdd((unsigned long long*)&s_sum[(__ffs((int)f) - 1) * g.K + k], (unsigned long long)v);
+        }
+      }
+      unsigned long long over = __ballot(n > kScoreListCap);
+      while (over) {  // wide clauses: the whole wave walks the include mask
+        const int src = __ffsll((long long)over) - 1;
+        over &= over - 1ull;
+        const int64_t cc = c0 + src;
+        const uint32_t* m = planes + (cc * np + np - 1) * g.W;
+        uint32_t f2 = live;
+        for (int64_t wb = 0; wb < g.W; wb += kWave) {
+          const int64_t wd = wb + lane;
+          for (uint32_t mw = wd < g.W ? m[wd] : 0u; mw; mw &= mw - 1u) f2 &= s_xw[wd * 32 + __ffs((int)mw) - 1];
+        }
+        for (int off = 32; off > 0; off >>= 1) f2 &= (uint32_t)__shfl_xor((int)f2, off);
+        if (f2 && lane < g.K) {
+          const long long v = (long long)w[cc * g.K + lane];
+          for (uint32_t f = f2; f; f &= f - 1u)
+            atomicAdd((unsigned long long*)&s_sum[(__ffs((int)f) - 1) * g.K + lane], (unsigned long long)v);
+        }
+      }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < ns * (int)g.K; j += blockDim.x)
+      if (s_sum[j] != 0) atomicAdd((unsigned long long*)&acc[e0 * g.K + j], (unsigned long long)s_sum[j]);
+  }
+}
+
 template <int MODE, bool SUM32>
 static hipError_t launch_tile(const uint32_t* planes, const int32_t* ninc, const float* w, const uint32_t* X,
                               int64_t N, const Geom& g, long long* acc, uint32_t* out, hipStream_t s) {
@@ -763,6 +858,10 @@ size_t score_lists_bytes(const Geom& g) {
   return (size_t)g.C * kScoreListCap * 2 + (size_t)g.C * 4;
 }
 
+size_t score_wide_bytes(const Geom& g) {
+  return score_wide_fits(g) ? (size_t)g.C * kScoreListCap * 2 + (size_t)g.C * 4 : 0;
+}
+
 hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_t* XT, int64_t N, const Geom& g,
                            void* scratch, long long* acc, hipStream_t s) {
   uint16_t* lists = (uint16_t*)scratch;
@@ -771,6 +870,26 @@ hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_
   const int64_t blocks = N * ((g.C + kScoreLmChunk - 1) / kScoreLmChunk);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
   score_lm_kernel<<<grid, 256, (size_t)(g.L * ((g.P + 31) / 32)) * 4, s>>>(planes, lists, nlit, w, XT, N, g, acc);
+  return hipGetLastError();
+}
+
+bool score_wide_fits(const Geom& g) {
+  return g.P == 1 && g.W > 64 && g.K <= kTileMaxK && g.L <= 65535 && g.W * 32 * 4 <= kWideLdsBytes;
+}
+
+hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint32_t* X, int64_t N, const Geom& g,
+                             void* scratch, long long* acc, hipStream_t s) {
+  uint16_t* lists = (uint16_t*)scratch;
+  int32_t* nlit = (int32_t*)(lists + g.C * kScoreListCap);
+  build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
+  // enough blocks to fill the device (two per CU fit): split the clauses when tiles are few
+  const int64_t tiles = (N + kWideTile - 1) / kWideTile;
+  const int64_t want = (512 + tiles - 1) / tiles, most = (g.C + 1023) / 1024;
+  const int64_t nch = want < most ? want : most;
+  const int64_t blocks = tiles * (nch > 0 ? nch : 1);
+  const int grid = blocks < 65536 ? (int)blocks : 65536;
+  score_wide_kernel<<<grid, 1024, (size_t)(g.W * 32) * 4, s>>>(planes, lists, nlit, w, X, N, g, nch > 0 ? nch : 1,
+                                                                acc);
   return hipGetLastError();
 }
 
