@@ -338,10 +338,11 @@ def test_inference_random_state(dim, patch_dim, classes, clauses):
     assert_packed_equal(tm.transform_patchwise(encX[:9], is_X_encoded=True, packed=True), ref_pw)
 
 
-def test_transform_in_chunks(monkeypatch):
+@pytest.mark.parametrize("cfg", [3, 5])  # several patches; one patch with 625-word clauses
+def test_transform_in_chunks(monkeypatch, cfg):
     """Samples go through transform in chunks (forced small here): ragged last chunk, the
     literal lists built once and reused."""
-    tm, ref, X, y, Xt, yt = pair(3, 30, 23, clauses=60)
+    tm, ref, X, y, Xt, yt = pair(cfg, 30, 23, clauses=60)
     encX = tm.encode(X)
     tm.fit(encX, y, is_X_encoded=True)
     ref.fit_encoded(encX, ref.encode_y_multiclass(y))

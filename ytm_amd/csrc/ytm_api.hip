@@ -627,8 +627,10 @@ int ytm_transform(ytm_model* m, const uint32_t* encX, int64_t N, int mode, uint3
   const Geom& g = m->g;
   const int64_t PW = (g.P + 31) / 32;
   const int64_t per_out = g.C * (mode == 0 ? 1 : (mode == 1 ? g.P : PW));  // uint32 per sample
-  const size_t lists_bytes = ytm::score_lists_bytes(g);
-  const bool lm = lists_bytes > 0;
+  const size_t lm_bytes = ytm::score_lists_bytes(g);
+  const bool lm = lm_bytes > 0;
+  const size_t wide_bytes = lm ? 0 : ytm::score_wide_bytes(g);  // one patch, wide clauses
+  const size_t lists_bytes = lm ? lm_bytes : wide_bytes;
   const int64_t per_in = g.P * g.W + (lm ? g.L * PW : 0);
   // Device buffers per pass stay within ~1 GiB; samples go through in chunks.
   int64_t chunk = ((int64_t)1 << 30) / ((per_out + per_in) * 4);
@@ -639,7 +641,7 @@ int ytm_transform(ytm_model* m, const uint32_t* encX, int64_t N, int mode, uint3
   hipError_t e = hipMalloc(&dX, (size_t)(chunk * g.P * g.W) * 4);
   if (e == hipSuccess) e = hipMalloc(&dO, (size_t)(chunk * per_out) * 4);
   if (e == hipSuccess && lm) e = hipMalloc(&dXT, (size_t)(chunk * g.L * PW) * 4);
-  if (e == hipSuccess && lm) e = hipMalloc(&dL, lists_bytes);
+  if (e == hipSuccess && lists_bytes) e = hipMalloc(&dL, lists_bytes);
   if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
   for (int64_t first = 0; e == hipSuccess && first < N; first += chunk) {
     const int64_t n = N - first < chunk ? N - first : chunk;
@@ -648,6 +650,8 @@ int ytm_transform(ytm_model* m, const uint32_t* encX, int64_t N, int mode, uint3
     if (e == hipSuccess && lm) {
       e = ytm::launch_transpose(dX, n, dXT, g, m->stream);
       if (e == hipSuccess) e = ytm::launch_transform_lm(m->d_planes, dXT, n, g, mode, dL, first > 0, dO, m->stream);
+    } else if (e == hipSuccess && wide_bytes) {
+      e = ytm::launch_transform_wide(m->d_planes, dX, n, g, dL, first > 0, dO, m->stream);
     } else if (e == hipSuccess) {
       e = ytm::launch_transform(m->d_planes, m->d_ninc, dX, n, g, mode, dO, m->stream);
     }

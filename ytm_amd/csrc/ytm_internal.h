@@ -49,6 +49,10 @@ hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t 
 // (N, C, ceil(P/32)).
 hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const uint32_t* X, int64_t N,
                             const Geom& g, int mode, uint32_t* out, hipStream_t s);
+// One patch and clauses wider than 64 words (score_wide_fits), all modes alike: scratch holds
+// score_wide_bytes(g), its literal lists built first unless lists_ready.
+hipError_t launch_transform_wide(const uint32_t* planes, const uint32_t* X, int64_t N, const Geom& g, void* scratch,
+                                 bool lists_ready, uint32_t* out, hipStream_t s);
 // The same on literal-major samples; scratch holds score_lists_bytes(g), its literal lists
 // built first unless lists_ready.
 hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64_t N, const Geom& g, int mode,

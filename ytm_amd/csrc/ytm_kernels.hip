@@ -749,16 +749,18 @@ hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s) {
 // empty clauses do not vote).  Clauses with more literals than the list holds are AND-ed
 // by the whole wave from their include masks.  With few tiles the clauses are split into
 // nch chunks over blocks; each block adds its chunk's exact sums into acc[e][k] (zeroed
-// before the launch).
+// before the launch).  OUT: clause outputs instead (transform and transform_patchwise with
+// their single patch, kernel.cu:346-394: an empty clause outputs 1), out[e][c], written by
+// the clause's lane for each sample of the tile.
 constexpr int kWideTile = 32;
 constexpr int64_t kWideLdsBytes = 96 * 1024;
 
-__global__ __launch_bounds__(1024) void score_wide_kernel(const uint32_t* __restrict__ planes,
-                                                          const uint16_t* __restrict__ lists,
-                                                          const int32_t* __restrict__ nlit,
-                                                          const float* __restrict__ w,
-                                                          const uint32_t* __restrict__ X, int64_t N, Geom g,
-                                                          int64_t nch, long long* __restrict__ acc) {
+template <bool OUT>
+__global__ __launch_bounds__(1024) void wide_kernel(const uint32_t* __restrict__ planes,
+                                                    const uint16_t* __restrict__ lists,
+                                                    const int32_t* __restrict__ nlit, const float* __restrict__ w,
+                                                    const uint32_t* __restrict__ X, int64_t N, Geom g, int64_t nch,
+                                                    long long* __restrict__ acc, uint32_t* __restrict__ out) {
   extern __shared__ uint32_t s_xw[];  // [W * 32]: word l = literal l over the tile's samples
   __shared__ long long s_sum[kWideTile * kTileMaxK];
   const int lane = lane_id();
@@ -793,7 +795,7 @@ __global__ __launch_bounds__(1024) void score_wide_kernel(const uint32_t* __rest
     for (int64_t c0 = cb + (int64_t)wave * kWave; c0 < ce; c0 += (int64_t)nwv * kWave) {
       const int64_t c = c0 + lane;
       const int n = c < ce ? nlit[c] : 0;
-      uint32_t fire = 0u;
+      uint32_t fire = (OUT && n == 0) ? live : 0u;  // empty clauses: output 1, no vote
       if (n > 0 && n <= kScoreListCap) {
         fire = live;
         const uint16_t* lst = lists + c * kScoreListCap;
@@ -803,7 +805,7 @@ __global__ __launch_bounds__(1024) void score_wide_kernel(const uint32_t* __rest
                   s_xw[q.z & 0xFFFFu] & s_xw[q.z >> 16] & s_xw[q.w & 0xFFFFu] & s_xw[q.w >> 16];
         }
       }
-      if (fire) {
+      if (!OUT && fire) {
         for (int k = 0; k < (int)g.K; ++k) {
           const long long v = (long long)w[c * g.K + k];
           for (uint32_t f = fire; f; f &= f - 1u)
@@ -822,16 +824,21 @@ __global__ __launch_bounds__(1024) void score_wide_kernel(const uint32_t* __rest
           for (uint32_t mw = wd < g.W ? m[wd] : 0u; mw; mw &= mw - 1u) f2 &= s_xw[wd * 32 + __ffs((int)mw) - 1];
         }
         for (int off = 32; off > 0; off >>= 1) f2 &= (uint32_t)__shfl_xor((int)f2, off);
-        if (f2 && lane < g.K) {
+        if (OUT && lane == src) fire = f2;
+        if (!OUT && f2 && lane < g.K) {
           const long long v = (long long)w[cc * g.K + lane];
           for (uint32_t f = f2; f; f &= f - 1u)
             atomicAdd((unsigned long long*)&s_sum[(__ffs((int)f) - 1) * g.K + lane], (unsigned long long)v);
         }
       }
+      if (OUT && c < ce)
+        for (int sm = 0; sm < ns; ++sm) out[(e0 + sm) * g.C + c] = (fire >> sm) & 1u;
     }
-    __syncthreads();
-    for (int j = threadIdx.x; j < ns * (int)g.K; j += blockDim.x)
-      if (s_sum[j] != 0) atomicAdd((unsigned long long*)&acc[e0 * g.K + j], (unsigned long long)s_sum[j]);
+    if (!OUT) {
+      __syncthreads();
+      for (int j = threadIdx.x; j < ns * (int)g.K; j += blockDim.x)
+        if (s_sum[j] != 0) atomicAdd((unsigned long long*)&acc[e0 * g.K + j], (unsigned long long)s_sum[j]);
+    }
   }
 }
 
@@ -888,8 +895,24 @@ hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint3
   const int64_t nch = want < most ? want : most;
   const int64_t blocks = tiles * (nch > 0 ? nch : 1);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
-  score_wide_kernel<<<grid, 1024, (size_t)(g.W * 32) * 4, s>>>(planes, lists, nlit, w, X, N, g, nch > 0 ? nch : 1,
-                                                                acc);
+  wide_kernel<false><<<grid, 1024, (size_t)(g.W * 32) * 4, s>>>(planes, lists, nlit, w, X, N, g, nch > 0 ? nch : 1,
+                                                                 acc, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_transform_wide(const uint32_t* planes, const uint32_t* X, int64_t N, const Geom& g, void* scratch,
+                                 bool lists_ready, uint32_t* out, hipStream_t s) {
+  uint16_t* lists = (uint16_t*)scratch;
+  int32_t* nlit = (int32_t*)(lists + g.C * kScoreListCap);
+  if (!lists_ready)
+    build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
+  const int64_t tiles = (N + kWideTile - 1) / kWideTile;
+  const int64_t want = (512 + tiles - 1) / tiles, most = (g.C + 1023) / 1024;
+  const int64_t nch = want < most ? want : most;
+  const int64_t blocks = tiles * (nch > 0 ? nch : 1);
+  const int grid = blocks < 65536 ? (int)blocks : 65536;
+  wide_kernel<true><<<grid, 1024, (size_t)(g.W * 32) * 4, s>>>(planes, lists, nlit, nullptr, X, N, g,
+                                                                nch > 0 ? nch : 1, nullptr, out);
   return hipGetLastError();
 }
 
