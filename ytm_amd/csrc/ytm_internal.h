@@ -36,7 +36,7 @@ hipError_t launch_score_parts_finish(const long long* parts, int64_t nch, const 
 size_t score_lists_bytes(const Geom& g);
 hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_t* XT, int64_t N, const Geom& g,
                            void* scratch, long long* acc, hipStream_t s);
-// One patch and clauses wider than 64 words: a tile of samples transposed in LDS, the
+// One patch and clauses wider than 16 words: a tile of samples transposed in LDS, the
 // clauses' literal lists AND-ed lane by lane; scratch holds score_wide_bytes(g); acc (zeroed
 // first) receives each sample's exact sums.
 bool score_wide_fits(const Geom& g);
@@ -49,7 +49,7 @@ hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t 
 // (N, C, ceil(P/32)).
 hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const uint32_t* X, int64_t N,
                             const Geom& g, int mode, uint32_t* out, hipStream_t s);
-// One patch and clauses wider than 64 words (score_wide_fits), all modes alike: scratch holds
+// One patch and clauses wider than 16 words (score_wide_fits), all modes alike: scratch holds
 // score_wide_bytes(g), its literal lists built first unless lists_ready.
 hipError_t launch_transform_wide(const uint32_t* planes, const uint32_t* X, int64_t N, const Geom& g, void* scratch,
                                  bool lists_ready, uint32_t* out, hipStream_t s);
