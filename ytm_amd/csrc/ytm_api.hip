@@ -31,6 +31,12 @@ struct ytm_model {
   int* d_err = nullptr;
   unsigned long long* d_slots = nullptr;
   size_t slots_bytes = 0;
+  // Scoring buffers kept between calls (grow-only): class-sum accumulators, float sums,
+  // literal lists.  Calls are synchronous, so a call never reuses a buffer still in use.
+  void* d_sacc = nullptr;
+  void* d_sout = nullptr;
+  void* d_slists = nullptr;
+  size_t sacc_bytes = 0, sout_bytes = 0, slists_bytes = 0;
   // Upper bound of |clause weight|: 1 after initialisation, the largest loaded magnitude
   // after ytm_set_weights, and + 1 per trained sample (a sample moves a weight by at most 1).
   double w_bound = 1.0;
@@ -124,6 +130,20 @@ int resolve_geometry(const ytm_params& p, Geom* out) {
   g.s_thr = !(scaled > 0.0) ? 0u : (scaled >= 16777216.0 ? (1u << 24) : (uint32_t)scaled);
   *out = g;
   return YTM_OK;
+}
+
+// A grow-only device buffer: *p holds at least bytes after a successful call.
+hipError_t ensure_buffer(void** p, size_t* have, size_t bytes) {
+  if (*have >= bytes && *p) return hipSuccess;
+  if (*p) {
+    const hipError_t e = hipFree(*p);
+    if (e != hipSuccess) return e;
+  }
+  *p = nullptr;
+  *have = 0;
+  const hipError_t e = hipMalloc(p, bytes > 0 ? bytes : 4);
+  if (e == hipSuccess) *have = bytes;
+  return e;
 }
 
 int ensure_slots(ytm_model* m, size_t bytes) {
@@ -282,7 +302,8 @@ int ytm_create(const ytm_params* params, ytm_model** out) {
 void ytm_destroy(ytm_model* m) {
   if (!m) return;
   if (m->stream) (void)hipStreamSynchronize(m->stream);
-  void* bufs[] = {m->d_planes, m->d_w, m->d_pw, m->d_bias, m->d_ninc, m->d_inv_rank, m->d_counters, m->d_err, m->d_slots};
+  void* bufs[] = {m->d_planes, m->d_w,    m->d_pw,   m->d_bias, m->d_ninc,  m->d_inv_rank,
+                  m->d_counters, m->d_err, m->d_slots, m->d_sacc, m->d_sout, m->d_slists};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   if (m->ev0) (void)hipEventDestroy(m->ev0);
@@ -570,16 +591,16 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   const Geom& g = m->g;
   const int64_t N = ds->N;
   if (N == 0) return YTM_OK;
-  long long* acc = nullptr;
-  float* dout = nullptr;
-  void* lists = nullptr;  // several patches, or one patch with wide clauses: the literal lists
   const size_t lm_bytes = ds->d_XT ? ytm::score_lists_bytes(g) : 0;
   const size_t wide_bytes = lm_bytes ? 0 : ytm::score_wide_bytes(g);
   const size_t lists_bytes = lm_bytes ? lm_bytes : wide_bytes;
   const int64_t chunks = lists_bytes ? 0 : ytm::score_tile_chunks(g);  // one patch: per-chunk sums
-  HIP_TRY(hipMalloc(&acc, (size_t)(N * g.K * (chunks ? chunks : 1)) * 8));
-  hipError_t e = hipMalloc(&dout, (size_t)(N * g.K) * 4);
-  if (e == hipSuccess && lists_bytes) e = hipMalloc(&lists, lists_bytes);
+  hipError_t e = ensure_buffer(&m->d_sacc, &m->sacc_bytes, (size_t)(N * g.K * (chunks ? chunks : 1)) * 8);
+  if (e == hipSuccess) e = ensure_buffer(&m->d_sout, &m->sout_bytes, (size_t)(N * g.K) * 4);
+  if (e == hipSuccess && lists_bytes) e = ensure_buffer(&m->d_slists, &m->slists_bytes, lists_bytes);
+  long long* acc = (long long*)m->d_sacc;
+  float* dout = (float*)m->d_sout;
+  void* lists = lists_bytes ? m->d_slists : nullptr;  // several patches, or one patch with wide clauses
   int rc = YTM_OK;
   if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
   if (e == hipSuccess && !chunks) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
@@ -604,9 +625,6 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (e == hipSuccess) e = hipEventElapsedTime(&ms, m->ev0, m->ev1);
   if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("score failed: ") + hipGetErrorString(e));
   m->stats.last_score_kernel_ms = ms;
-  if (acc) (void)hipFree(acc);
-  if (dout) (void)hipFree(dout);
-  if (lists) (void)hipFree(lists);
   return rc;
 }
 
