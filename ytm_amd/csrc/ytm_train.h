@@ -169,69 +169,28 @@ __device__ __forceinline__ uint32_t all_patches_word(const Geom& g) {
 
 // Included literals of a clause (include mask m, W words), in increasing order, written to
 // list[0, n) when n <= cap, the entries from n to the next multiple of 8 repeating literal
-// n-1 (cap a multiple of 8).  Returns n, the include count.  Lane j of each round of 64
-// finds the j-th included literal: the word holding it from a walk over the words' prefix
-// counts, then its bit by a select.  Wave-uniform.
+// n-1 (cap a multiple of 8).  Returns n, the include count.  Wave-uniform.
 __device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* list, int cap) {
+  // 64 words at a time, one per lane: lane w writes its word's included literals from its
+  // prefix-sum offset, lowest bit first, so the list is in increasing literal order
   const int lane = lane_id();
-  if (g.W <= kWave) {
-    // one word per lane: lane w writes its word's included literals from its prefix offset,
-    // lowest bit first, so the list is in increasing literal order as below
-    uint32_t mv = lane < g.W ? m[lane] : 0u;
-    const int pc = __popc(mv);
-    const int incl = wave_inclusive_scan(pc);
-    const int total = lane_value(incl, kWave - 1);
-    int pos = incl - pc;
-    const unsigned long long nz = __ballot(mv != 0u);
-    const int hi = nz ? 63 - __clzll((long long)nz) : 0;  // lane of the last included literal
-    const int last = lane_value(32 * lane + 31 - __clz((int)(mv | 1u)), hi);
-    while (mv) {
-      const int b = __ffs((int)mv) - 1;
-      if (pos < cap) list[pos] = (uint16_t)(32 * lane + b);
-      ++pos;
-      mv &= mv - 1u;
-    }
-    if (total > 0 && total <= cap) {
-      const int pad_end = ((total + 7) & ~7) < cap ? ((total + 7) & ~7) : cap;
-      for (int p = total + lane; p < pad_end; p += kWave) list[p] = (uint16_t)last;
-    }
-    return total;
-  }
   int total = 0, last = 0;
   for (int64_t wb = 0; wb < g.W; wb += kWave) {
-    const uint32_t mv = wb + lane < g.W ? m[wb + lane] : 0u;
+    const int64_t w = wb + lane;
+    uint32_t mv = w < g.W ? m[w] : 0u;
     const int pc = __popc(mv);
     const int incl = wave_inclusive_scan(pc);
     const int tot = lane_value(incl, kWave - 1);
-    const int nw = (int)(g.W - wb < kWave ? g.W - wb : kWave);
-    for (int jb = 0; jb < tot; jb += kWave) {
-      const int j = jb + lane;
-      uint32_t mw = 0u;
-      int q = 0, ex = 0, before = 0;
-      for (int w = 0; w < nw; ++w) {
-        const int after = lane_value(incl, w);
-        if (before <= j && j < after) {
-          q = w;
-          ex = before;
-          mw = (uint32_t)lane_value((int)mv, w);
-        }
-        before = after;
-      }
-      int r = j - ex, pos = 0;
-      uint32_t v = mw;
-#pragma unroll
-      for (int width = 16; width > 0; width >>= 1) {
-        const int lowc = __popc(v & ((1u << width) - 1u));
-        if (r >= lowc) {
-          r -= lowc;
-          v >>= width;
-          pos += width;
-        }
-      }
-      const int lit = (int)(32 * (wb + q)) + pos;
-      const int cnt = tot - jb < kWave ? tot - jb : kWave;
-      if (j < tot && total + j < cap) list[total + j] = (uint16_t)lit;
-      last = lane_value(lit, cnt - 1);
+    if (tot == 0) continue;
+    const unsigned long long nz = __ballot(mv != 0u);
+    const int hi = 63 - __clzll((long long)nz);  // lane of the chunk's last included literal
+    last = lane_value((int)(32 * w) + 31 - __clz((int)(mv | 1u)), hi);
+    int pos = total + incl - pc;
+    while (mv) {
+      const int b = __ffs((int)mv) - 1;
+      if (pos < cap) list[pos] = (uint16_t)(32 * w + b);
+      ++pos;
+      mv &= mv - 1u;
     }
     total += tot;
   }
