@@ -338,6 +338,33 @@ def test_inference_random_state(dim, patch_dim, classes, clauses):
     assert_packed_equal(tm.transform_patchwise(encX[:9], is_X_encoded=True, packed=True), ref_pw)
 
 
+@pytest.mark.parametrize("global_state", [False, True])
+def test_fit_random_state_wide_one_patch(monkeypatch, global_state):
+    """Training from a random state of a one-patch model with 94-word clauses, some of which
+    include ~300 literals, on the resident and the global kernel."""
+    if global_state:
+        monkeypatch.setenv("YTM_TRAIN_GLOBAL", "1")
+    dim, classes, clauses = (1500, 1, 1), 2, 60
+    kw = dict(number_of_clauses_per_class=clauses, T=50, s=5.0, dim=dim, n_classes=classes, seed=7)
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(clauses, 50, 5.0, dim, classes, seed=7)
+    rng = np.random.default_rng(13)
+    L = tm.number_of_literals
+    include_p = np.where(rng.random(tm.number_of_clauses) < 0.1, 0.0, 4.0 / L)
+    include_p[rng.random(tm.number_of_clauses) < 0.1] = 300.0 / L
+    random_state(tm, ref, rng, include_p)
+    X = (rng.random((80, 1500)) < 0.9).astype(np.uint32)  # dense, so that wide clauses can fire
+    y = rng.integers(0, classes, size=80).astype(np.uint32)
+    encX = tm.encode(X)
+    for epoch in range(2):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+    if global_state:
+        assert tm.stats()["train_kind"] == 1
+
+
 @pytest.mark.parametrize("cfg", [3, 5])  # several patches; one patch with 625-word clauses
 def test_transform_in_chunks(monkeypatch, cfg):
     """Samples go through transform in chunks (forced small here): ragged last chunk, the
