@@ -143,6 +143,18 @@ int ytm_fit(ytm_model *m, const uint32_t *encX, const int32_t *encY, int64_t N,
 /* score: BaseTM._score_batch (src/cutm/base.py:375-420; kernel.cu:319-343).
  * class_sums: float (N, classes) = bias + sum of weights of non-empty firing clauses. */
 int ytm_score_dataset(ytm_model *m, const ytm_dataset *ds, float *class_sums);
+/* ytm_score_dataset without any device allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  d_class_sums is a DEVICE pointer to
+ * float (N, classes), written with the same values ytm_score_dataset returns.  The
+ * kernels' literal lists and int64 class-sum accumulators live in a static per-GPU scratch
+ * array of YTM_NOALLOC_SCRATCH_BYTES (32 MiB; each GPU that runs this holds it until the
+ * process ends); samples go through in passes that fit it.  YTM_EINVAL when the model's
+ * lists plus one sample's accumulators do not fit (e.g. one-patch models of more than
+ * about 65000 wide clauses).  Calls on one GPU share the array, so overlapping calls
+ * would race: the library serialises them per GPU with a lock.  Synchronous on return. */
+#define YTM_NOALLOC_SCRATCH_BYTES (32u << 20)
+int ytm_score_dataset_noalloc(ytm_model *m, const ytm_dataset *ds, float *d_class_sums);
 int ytm_score(ytm_model *m, const uint32_t *encX, int64_t N, float *class_sums);
 
 /* transform / transform_patchwise (src/cutm/base.py:465-542; kernel.cu:346-394).

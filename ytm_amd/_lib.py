@@ -75,6 +75,7 @@ SIGNATURES = {
     "ytm_fit_dataset": (ctypes.c_int, [_P, _P, _I64, _I64, _P, _P]),
     "ytm_fit": (ctypes.c_int, [_P, _P, _P, _I64, _P, _P]),
     "ytm_score_dataset": (ctypes.c_int, [_P, _P, _P]),
+    "ytm_score_dataset_noalloc": (ctypes.c_int, [_P, _P, _P]),
     "ytm_score": (ctypes.c_int, [_P, _P, _I64, _P]),
     "ytm_transform": (ctypes.c_int, [_P, _P, _I64, ctypes.c_int, _P]),
     "ytm_get_ta_state": (ctypes.c_int, [_P, _P]),

@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -586,39 +587,100 @@ int ytm_fit(ytm_model* m, const uint32_t* encX, const int32_t* encY, int64_t N, 
   return rc;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Which scoring kernel a dataset takes, and the device buffers it needs besides the output:
+// literal lists (lists_bytes, several patches or one patch with wide clauses) and the int64
+// class-sum accumulators, acc_per_sample bytes per sample (per-chunk slices for the tiled
+// one-patch scorer, chunks > 0).
+struct ScorePlan {
+  size_t lists_bytes;
+  bool wide;
+  int64_t chunks;
+  size_t acc_per_sample;
+};
+
+ScorePlan score_plan(const Geom& g, bool has_xt) {
+  ScorePlan p{};
+  const size_t lm_bytes = has_xt ? ytm::score_lists_bytes(g) : 0;
+  const size_t wide_bytes = lm_bytes ? 0 : ytm::score_wide_bytes(g);
+  p.lists_bytes = lm_bytes ? lm_bytes : wide_bytes;
+  p.wide = wide_bytes > 0;
+  p.chunks = p.lists_bytes ? 0 : ytm::score_tile_chunks(g);
+  p.acc_per_sample = (size_t)g.K * (size_t)(p.chunks ? p.chunks : 1) * 8;
+  return p;
+}
+
+// Class sums of N samples (X [N][P][W], XT its literal-major copy or null) into out (device
+// float [N][K]), with the caller's buffers acc (plan.acc_per_sample * N bytes) and lists
+// (plan.lists_bytes).  Enqueued on the model's stream; the include counts are current.
+hipError_t score_samples(ytm_model* m, const ScorePlan& plan, const uint32_t* X, const uint32_t* XT, int64_t N,
+                         long long* acc, void* lists, float* out) {
+  const Geom& g = m->g;
+  hipError_t e = hipSuccess;
+  if (!plan.chunks) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
+  if (e != hipSuccess) return e;
+  if (plan.wide)
+    e = ytm::launch_score_wide(m->d_planes, m->d_w, X, N, g, lists, acc, m->stream);
+  else if (plan.lists_bytes)
+    e = ytm::launch_score_lm(m->d_planes, m->d_w, XT, N, g, lists, acc, m->stream);
+  else if (plan.chunks)
+    e = ytm::launch_score_tile(m->d_planes, m->d_ninc, m->d_w, X, N, g, acc, m->w_bound, m->stream);
+  else
+    e = ytm::launch_score(m->d_planes, m->d_ninc, m->d_w, X, N, g, acc, m->stream);
+  if (e != hipSuccess) return e;
+  return plan.chunks ? ytm::launch_score_parts_finish(acc, plan.chunks, m->d_bias, N, g, out, m->stream)
+                     : ytm::launch_score_finish(acc, m->d_bias, N, g, out, m->stream);
+}
+
+// ---- Scratch of the allocation-free scoring entry point: one static device array per GPU
+// (each device that runs it holds its own copy, at its own address, until the process
+// ends).  Host code never passes the array's name to a kernel: the name is a host-side
+// stand-in, not a device address.  Its device address is looked up once per device, with
+// that device current, and kept in g_scratch_ptr.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu[kMaxDevices];  // held for a whole call: calls on one GPU share the array
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this device's scratch array (the model's device must be current).
+int scratch_address(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices) return fail(YTM_EINVAL, "device index out of range for the scratch table");
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(YTM_EHIP, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return YTM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (!m || !ds || ds->m != m || (ds->N > 0 && !class_sums)) return fail(YTM_EINVAL, "bad score arguments");
   const Geom& g = m->g;
   const int64_t N = ds->N;
   if (N == 0) return YTM_OK;
-  const size_t lm_bytes = ds->d_XT ? ytm::score_lists_bytes(g) : 0;
-  const size_t wide_bytes = lm_bytes ? 0 : ytm::score_wide_bytes(g);
-  const size_t lists_bytes = lm_bytes ? lm_bytes : wide_bytes;
-  const int64_t chunks = lists_bytes ? 0 : ytm::score_tile_chunks(g);  // one patch: per-chunk sums
-  hipError_t e = ensure_buffer(&m->d_sacc, &m->sacc_bytes, (size_t)(N * g.K * (chunks ? chunks : 1)) * 8);
+  const ScorePlan plan = score_plan(g, ds->d_XT != nullptr);
+  hipError_t e = ensure_buffer(&m->d_sacc, &m->sacc_bytes, (size_t)N * plan.acc_per_sample);
   if (e == hipSuccess) e = ensure_buffer(&m->d_sout, &m->sout_bytes, (size_t)(N * g.K) * 4);
-  if (e == hipSuccess && lists_bytes) e = ensure_buffer(&m->d_slists, &m->slists_bytes, lists_bytes);
-  long long* acc = (long long*)m->d_sacc;
+  if (e == hipSuccess && plan.lists_bytes) e = ensure_buffer(&m->d_slists, &m->slists_bytes, plan.lists_bytes);
   float* dout = (float*)m->d_sout;
-  void* lists = lists_bytes ? m->d_slists : nullptr;  // several patches, or one patch with wide clauses
   int rc = YTM_OK;
   if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
-  if (e == hipSuccess && !chunks) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
   if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
-  if (e == hipSuccess) {
-    if (wide_bytes)
-      e = ytm::launch_score_wide(m->d_planes, m->d_w, ds->d_X, N, g, lists, acc, m->stream);
-    else if (lists)
-      e = ytm::launch_score_lm(m->d_planes, m->d_w, ds->d_XT, N, g, lists, acc, m->stream);
-    else if (chunks)
-      e = ytm::launch_score_tile(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->w_bound, m->stream);
-    else
-      e = ytm::launch_score(m->d_planes, m->d_ninc, m->d_w, ds->d_X, N, g, acc, m->stream);
-  }
-  if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
   if (e == hipSuccess)
-    e = chunks ? ytm::launch_score_parts_finish(acc, chunks, m->d_bias, N, g, dout, m->stream)
-               : ytm::launch_score_finish(acc, m->d_bias, N, g, dout, m->stream);
+    e = score_samples(m, plan, ds->d_X, ds->d_XT, N, (long long*)m->d_sacc, plan.lists_bytes ? m->d_slists : nullptr,
+                      dout);
+  if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(class_sums, dout, (size_t)(N * g.K) * 4, hipMemcpyDeviceToHost, m->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
   float ms = 0.0f;
@@ -626,6 +688,43 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("score failed: ") + hipGetErrorString(e));
   m->stats.last_score_kernel_ms = ms;
   return rc;
+}
+
+int ytm_score_dataset_noalloc(ytm_model* m, const ytm_dataset* ds, float* d_class_sums) {
+  if (!m || !ds || ds->m != m || (ds->N > 0 && !d_class_sums)) return fail(YTM_EINVAL, "bad score arguments");
+  const Geom& g = m->g;
+  const int64_t N = ds->N;
+  if (N == 0) return YTM_OK;
+  const ScorePlan plan = score_plan(g, ds->d_XT != nullptr);
+  const size_t lists_room = (plan.lists_bytes + 255) & ~(size_t)255;  // the sums start 256-byte aligned
+  if (lists_room + plan.acc_per_sample > kNoAllocScratchBytes)
+    return fail(YTM_EINVAL, "model too large for the allocation-free scorer: it needs " +
+                                std::to_string(lists_room + plan.acc_per_sample) + " bytes of scratch for one sample, " +
+                                "the scratch holds " + std::to_string(kNoAllocScratchBytes));
+  if (m->device < 0 || m->device >= kMaxDevices) return fail(YTM_EINVAL, "device index out of range for the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu[m->device]);
+  void* base = nullptr;
+  int rc = scratch_address(m->device, &base);
+  if (rc) return rc;
+  void* lists = plan.lists_bytes ? base : nullptr;
+  long long* acc = (long long*)((unsigned char*)base + lists_room);
+  // samples per pass: as many as the accumulators of the rest of the scratch hold
+  const int64_t per_pass = (int64_t)((kNoAllocScratchBytes - lists_room) / plan.acc_per_sample);
+  const int64_t PW = (g.P + 31) / 32;
+  hipError_t e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
+  if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
+  for (int64_t first = 0; e == hipSuccess && first < N; first += per_pass) {
+    const int64_t n = N - first < per_pass ? N - first : per_pass;
+    e = score_samples(m, plan, ds->d_X + first * g.P * g.W, ds->d_XT ? ds->d_XT + first * g.L * PW : nullptr, n, acc,
+                      lists, d_class_sums + first * g.K);
+  }
+  if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, m->ev0, m->ev1);
+  if (e != hipSuccess) return fail(YTM_EHIP, std::string("score failed: ") + hipGetErrorString(e));
+  m->stats.last_score_kernel_ms = ms;
+  return YTM_OK;
 }
 
 int ytm_score(ytm_model* m, const uint32_t* encX, int64_t N, float* class_sums) {
