@@ -172,11 +172,12 @@ def main() -> int:
         byts.append(train_bytes_per_launch(tm, N, st["last_fit_updates"]))
         log(f"[bench] step {s + 1}: wall {walls[-1]:.3f}s kernel {kern[-1]:.1f}ms updates {st['last_fit_updates']} "
             f"({st['last_fit_updates'] / N:.1f}/sample) workgroups {st['train_workgroups']} "
-            f"kind {st['train_kind']} wait {st['last_fit_wait_frac']:.3f}")
+            f"kind {st['train_kind']} wait {st['last_fit_wait_frac']:.3f} "
+            f"feedback samples {st['last_fit_feedback_samples']} evaluations {st['last_fit_evaluations']}")
         if os.environ.get("YTM_TRAIN_PROFILE"):
-            names = (("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier", "step1-slowest-wave")
-                     if st["train_kind"] == 0
-                     else ("A", "barrier", "exchange", "barrier", "D", "barrier"))
+            names = {0: ("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier", "step1-slowest-wave"),
+                     3: ("stream", "drain", "decide", "apply")}.get(
+                         st["train_kind"], ("A", "barrier", "exchange", "barrier", "D", "barrier"))
             log("[bench]   phase us/sample (wave 0): "
                 + " ".join(f"{n} {v:.2f}" for n, v in zip(names, st["last_fit_phase_us"])))
 

@@ -79,7 +79,8 @@ typedef struct ytm_stats {
     double last_fit_wait_frac;   /* share of the training kernel's time workgroups spent
                                     waiting for the per-sample class sums */
     int32_t train_kind;          /* 0 = clause state resident in LDS, 1 = global (one
-                                    patch), 2 = global (several patches) */
+                                    patch), 2 = global (several patches), 3 = resident and
+                                    streaming (one patch) */
     int32_t train_specialised;   /* 1 when the last fit ran a training kernel compiled at run
                                     time for this model's geometry (hipRTC), 0 when it ran the
                                     built-in kernel (YTM_JIT=0, or the compile was unavailable) */
@@ -91,6 +92,15 @@ typedef struct ytm_stats {
                                     barrier).  YTM_TRAIN_PROFILE=2 / =3 restrict that last
                                     resident slot to the next sample's evaluation / its
                                     evaluation and the staging of the sample after it */
+    uint64_t last_fit_feedback_samples; /* samples of the last fit at which some class had an
+                                    update probability above zero (the streaming kernel stops
+                                    there to apply feedback); the sample count for the others */
+    uint64_t last_fit_evaluations; /* clause evaluations of a sample per workgroup, averaged:
+                                    the sample count plus the speculative ones discarded at
+                                    stops (streaming kernel); the sample count for the others */
+    int32_t last_fit_stream;     /* 1 when the last fit ran the streaming kernel (train_kind
+                                    is then 3) */
+    int32_t reserved;
 } ytm_stats;
 
 /* Thread-local description of the last failure. */
@@ -109,8 +119,8 @@ int ytm_set_seed(ytm_model *m, uint64_t seed);
 /* Compile (and cache for this process) the training kernel specialised for the geometry
  * of *params and the launch shape used on a device with compute_units CUs (0: 256, an
  * MI355X), without touching a GPU.  train_kind as in ytm_stats (0 resident: one patch, or
- * several with ceil(P/32) <= 64; 1 global one patch; 2 global several patches); injected != 0
- * for the injected-draw variant.
+ * several with ceil(P/32) <= 64; 1 global one patch; 2 global several patches; 3 streaming:
+ * one patch, coalesced, counter stream only); injected != 0 for the injected-draw variant.
  * The counterpart of the per-model kernel compile in BaseTM.__init__
  * (src/cutm/base.py:129-159); ytm_fit compiles on first use anyway, so calling this is
  * optional (warm-up, or checking that the compiler is available).  YTM_EHIP with the

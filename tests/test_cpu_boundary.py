@@ -65,7 +65,10 @@ def test_specialised_training_kernels_compile(cfg):
     kw = workloads.make(cfg, 2, 2)[4]
     for injected in (False, True):
         kinds = MultiClassTM.compile_kernels(**kw, injected=injected)
-        assert kinds == ([0, 2] if cfg in (3, 4) else [0, 1])
+        # the streaming kernel (3): one patch, counter stream, at most 64 clauses per workgroup
+        # on 256 CUs, clause state within LDS (configs 1 and 2; not config 5's 10000 wide clauses)
+        expect = [0, 2] if cfg in (3, 4) else ([0, 1, 3] if cfg in (1, 2) and not injected else [0, 1])
+        assert kinds == expect
 
 
 def test_compile_entry_point_rejects_bad_kind():
@@ -78,6 +81,8 @@ def test_compile_entry_point_rejects_bad_kind():
     assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 2, 0, 0) == 1  # 2: several patches only
     assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 7, 0, 0) == 1
     assert b"train_kind" in _lib.lib.ytm_last_error()
+    assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 3, 1, 0) == 1  # streaming: counter stream only
+    assert b"streaming" in _lib.lib.ytm_last_error()
     assert _lib.lib.ytm_compile_train_kernel(ctypes.byref(params), 0, 0, -1) == 1
     assert b"compute_units" in _lib.lib.ytm_last_error()
 

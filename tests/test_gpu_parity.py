@@ -125,6 +125,44 @@ def test_fit_builtin_kernels(monkeypatch, cfg, n, clauses, global_state, inject)
         assert_state_equal(tm, ref, f"epoch {epoch}")
 
 
+@pytest.mark.parametrize("cfg,n,clauses,epochs", [(1, 3000, None, 2), (2, 300, None, 2), (2, 200, 60, 3)])
+def test_fit_resident_kernel_counter_stream(monkeypatch, cfg, n, clauses, epochs):
+    """One-patch models on the resident kernel (the streaming kernel switched off)."""
+    monkeypatch.setenv("YTM_TRAIN_STREAM", "0")
+    tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    for epoch in range(epochs):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, encY)
+        assert tm.stats()["train_kind"] == 0 and tm.stats()["last_fit_stream"] == 0
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+
+
+@pytest.mark.parametrize("wgs,threads", [("", ""), ("7", ""), ("31", "512"), ("64", "256")])
+def test_fit_stream_launch_shapes(monkeypatch, wgs, threads):
+    """The streaming kernel (one patch, counter stream) against the oracle over several
+    epochs, as training moves from feedback on most samples to feedback on few, for several
+    grids (50 clauses per workgroup down to 3) and workgroup sizes."""
+    monkeypatch.setenv("YTM_TRAIN_WGS", wgs)
+    monkeypatch.setenv("YTM_TRAIN_THREADS", threads)
+    tm, ref, X, y, *_ = pair(2, 2000, clauses=200)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    for epoch in range(4):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, encY)
+        st = tm.stats()
+        assert st["last_fit_stream"] == 1 and st["train_kind"] == 3
+        assert st["last_fit_updates"] == upd, f"update count epoch {epoch}"
+        assert 0 < st["last_fit_feedback_samples"] <= 2000
+        assert st["last_fit_evaluations"] >= 2000
+        print(f"[stream] wgs={wgs or 'default'} epoch {epoch}: feedback samples {st['last_fit_feedback_samples']}, "
+              f"evaluations {st['last_fit_evaluations']}, updates {upd}", flush=True)
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+
+
 def test_specialised_kernel_is_used():
     tm, ref, X, y, *_ = pair(2, 20)
     tm.fit(tm.encode(X), y, is_X_encoded=True)

@@ -55,6 +55,10 @@ class YtmStats(ctypes.Structure):
         ("train_kind", ctypes.c_int32),
         ("train_specialised", ctypes.c_int32),
         ("last_fit_phase_us", ctypes.c_double * 8),
+        ("last_fit_feedback_samples", ctypes.c_uint64),
+        ("last_fit_evaluations", ctypes.c_uint64),
+        ("last_fit_stream", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

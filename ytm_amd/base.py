@@ -196,6 +196,10 @@ class BaseTM:
         kinds = [0, 1] if P == 1 else ([0, 2] if (P + 31) // 32 <= 64 else [2])
         for kind in kinds:
             check(lib.ytm_compile_train_kernel(ctypes.byref(params), kind, int(bool(injected)), int(compute_units)))
+        # the streaming kernel (one patch, counter stream), when the model fits its shape
+        if P == 1 and not injected and lib.ytm_compile_train_kernel(ctypes.byref(params), 3, 0,
+                                                                     int(compute_units)) == _lib.YTM_OK:
+            kinds.append(3)
         return kinds
 
     def _gpu_init(self) -> None:

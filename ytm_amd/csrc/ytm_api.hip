@@ -234,6 +234,41 @@ void set_mask_lds(Geom* g, ytm::TrainKind kind, int cpw) {
   }
 }
 
+// The streaming kernel (train_stream_body) takes one-patch models with coalesced classes in
+// the counter stream when every workgroup's clauses fit one lane each and their state fits
+// LDS: grid ceil(C / 64) (YTM_TRAIN_WGS may raise it, up to C), 16 waves (YTM_TRAIN_THREADS
+// overrides).  False when the model does not fit that shape on `cus` compute units.
+bool stream_shape(const Geom& mg, int cus, Geom* out) {
+  if (mg.P != 1 || !mg.coalesced) return false;
+  int64_t G = (mg.C + ytm::kStreamClauses - 1) / ytm::kStreamClauses;
+  if (const char* e = std::getenv("YTM_TRAIN_WGS"))
+    if (std::atoi(e) > 0) G = std::max<int64_t>(G, std::min<int64_t>(std::atoi(e), mg.C));
+  if (G > cus || G > mg.C) return false;
+  Geom g = mg;
+  const char* envt = std::getenv("YTM_TRAIN_THREADS");
+  const int t = envt ? std::atoi(envt) : 0;
+  g.threads = (t >= 128 && t <= 1024 && t % 64 == 0) ? t : 1024;
+  g.grid = (int)G;
+  g.group_size = (int)G;
+  g.groups = 1;
+  g.list_cap = 0;
+  g.mask_lds = 0;
+  if (ytm::stream_lds_bytes(g, std::max(g.threads, ytm::kTrainThreads)) > ytm::kResidentLdsLimit) return false;
+  *out = g;
+  return true;
+}
+
+// Whether a fit of `count` samples takes the streaming kernel: the counter stream (not
+// injected draws), clause state not forced to global memory, the shape above, and int32
+// partial class sums exact (every weight the launch can reach, times 64, below 2^31).
+// YTM_TRAIN_STREAM=0 turns it off.
+bool stream_geometry(const ytm_model* m, bool inject, bool force_global, int64_t count, Geom* out) {
+  const char* env = std::getenv("YTM_TRAIN_STREAM");
+  if ((env && std::atoi(env) == 0) || inject || force_global) return false;
+  if (64.0 * (m->w_bound + (double)count) >= 2147483648.0) return false;
+  return stream_shape(m->g, m->cus, out);
+}
+
 ytm::TrainKind choose_train_kind(Geom* g, int cpw, bool force_global) {
   ytm::TrainKind kind = g->P == 1 ? ytm::TrainKind::kGlobalVanilla : ytm::TrainKind::kGlobalConv;
   if (!force_global && (g->P == 1 || ytm::literal_major(*g))) {
@@ -315,11 +350,21 @@ void ytm_destroy(ytm_model* m) {
 
 int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injected, int compute_units) {
   if (!params) return fail(YTM_EINVAL, "null params");
-  if (train_kind < 0 || train_kind > 2) return fail(YTM_EINVAL, "train_kind must be 0, 1 or 2");
+  if (train_kind < 0 || train_kind > 3) return fail(YTM_EINVAL, "train_kind must be 0, 1, 2 or 3");
   if (compute_units < 0) return fail(YTM_EINVAL, "compute_units must be >= 0");
   Geom model;
   int rc = resolve_geometry(*params, &model);
   if (rc) return rc;
+  if (train_kind == 3) {
+    Geom gs;
+    if (injected || !stream_shape(model, compute_units > 0 ? compute_units : 256, &gs))
+      return fail(YTM_EINVAL, "train_kind 3 (streaming) is for one-patch models with coalesced classes in the "
+                              "counter stream, at most 64 clauses per workgroup");
+    std::vector<char> code;
+    std::string why;
+    if (!ytm::jit_compile(gs, ytm::TrainKind::kStream, false, &code, &why)) return fail(YTM_EHIP, why);
+    return YTM_OK;
+  }
   int cpw;
   Geom g = train_geometry(model, compute_units > 0 ? compute_units : 256, &cpw);
   const bool valid = train_kind == 1 ? g.P == 1 : train_kind == 2 ? g.P > 1 : (g.P == 1 || ytm::literal_major(g));
@@ -436,14 +481,25 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   m->stats.last_fit_kernel_ms = 0.0;
   m->stats.last_fit_launches = 0;
   if (count == 0) return YTM_OK;
-  int cpw;
-  Geom g = train_geometry(m->g, m->cus, &cpw);  // the training kernels read both
-  const int grid = g.grid, D = g.groups;
   const bool inj = inject != nullptr;
   const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
-  const ytm::TrainKind kind = choose_train_kind(&g, cpw, force_global && std::atoi(force_global) > 0);
-  const int rng_slots = kind == ytm::TrainKind::kResident ? ytm::train_rng_slots(cpw, g) : 0;
-  const size_t lds = ytm::train_lds_bytes(kind, cpw, rng_slots, g);
+  const bool global = force_global && std::atoi(force_global) > 0;
+  int cpw;
+  Geom g;
+  ytm::TrainKind kind;
+  int rng_slots = 0;
+  size_t lds = 0;
+  if (stream_geometry(m, inj, global, count, &g)) {
+    kind = ytm::TrainKind::kStream;
+    cpw = ytm::kStreamClauses;
+    lds = ytm::stream_lds_bytes(g, g.threads);
+  } else {
+    g = train_geometry(m->g, m->cus, &cpw);  // the training kernels read both
+    kind = choose_train_kind(&g, cpw, global);
+    rng_slots = kind == ytm::TrainKind::kResident ? ytm::train_rng_slots(cpw, g) : 0;
+    lds = ytm::train_lds_bytes(kind, cpw, rng_slots, g);
+  }
+  const int grid = g.grid, D = g.groups;
   // Kernel specialised for this model's geometry (hipRTC), else the built-in one.
   // YTM_JIT=0 selects the built-in kernel; YTM_JIT=2 makes an unavailable compile an error.
   hipFunction_t jit_fn = nullptr;
@@ -468,7 +524,8 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   // injected mode, by the size of the injected block buffer (<= 1 GiB).
   const int64_t ks = (g.K + 15) & ~(int64_t)15;
   const int64_t slot_stride = D == 1 ? ks : (2 * (int64_t)D + 1) * ks;
-  const int64_t slot_row = slot_stride * 8;
+  // the streaming kernel uses up to stream_rows(n) rows of ks words for n samples
+  const int64_t slot_row = kind == ytm::TrainKind::kStream ? ytm::stream_rows(1) * ks * 8 : slot_stride * 8;
   int64_t per_launch = std::max<int64_t>(1, ((int64_t)256 << 20) / slot_row);
   const int64_t block = g.C * g.P + 2 * g.C * g.K + g.C * g.K * g.L;
   if (inj) per_launch = std::min<int64_t>(per_launch, std::max<int64_t>(1, ((int64_t)1 << 30) / (block * 4)));
@@ -514,7 +571,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     const int64_t n = std::min(per_launch, count - s);
     if (inj)
       FIT_TRY(hipMemcpyAsync(d_inj, inject + s * block, (size_t)(n * block) * 4, hipMemcpyHostToDevice, m->stream));
-    FIT_TRY(ytm::launch_fill_u64(m->d_slots, n * slot_stride, m->stream));
+    FIT_TRY(ytm::launch_fill_u64(m->d_slots, n * (slot_row / 8), m->stream));
     ytm::TrainArgs a{};
     a.planes = m->d_planes;
     a.weights = m->d_w;
@@ -563,6 +620,9 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   // phase ticks are summed over workgroups and samples: average microseconds per sample
   for (int j = 0; j < 8; ++j) m->stats.last_fit_phase_us[j] = (double)cnt[4 + j] / 100.0 / (double)grid / (double)count;
   const unsigned long long upd = cnt[0];
+  m->stats.last_fit_stream = kind == ytm::TrainKind::kStream;
+  m->stats.last_fit_feedback_samples = kind == ytm::TrainKind::kStream ? cnt[12] : (uint64_t)count;
+  m->stats.last_fit_evaluations = kind == ytm::TrainKind::kStream ? cnt[13] / (uint64_t)grid : (uint64_t)count;
 #undef FIT_TRY
   m->stats.last_fit_wait_frac = cnt[2] ? (double)cnt[1] / (double)cnt[2] : 0.0;
   m->stats.train_kind = (int32_t)kind;

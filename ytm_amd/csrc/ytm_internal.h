@@ -70,11 +70,14 @@ hipError_t launch_collapse_bins(const uint32_t* B, int64_t rows, int64_t width, 
 constexpr size_t kResidentLdsLimit = 150 * 1024;
 
 // Training kernel variants: clause state resident in LDS (one patch), or kept in global
-// memory (one patch / several patches).
-enum class TrainKind { kResident, kGlobalVanilla, kGlobalConv };
+// memory (one patch / several patches); kStream: one patch, clause state resident in LDS,
+// class sums of the samples ahead exchanged speculatively (train_stream_body).
+enum class TrainKind { kResident, kGlobalVanilla, kGlobalConv, kStream };
 hipError_t train_occupancy(TrainKind kind, bool inject, size_t lds_bytes, int* blocks_per_cu);
 hipError_t launch_train(const TrainArgs& a, int grid, size_t lds_bytes, TrainKind kind, bool inject, hipStream_t s);
 size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g);
+// LDS of the streaming kernel for a workgroup of `threads` threads.
+size_t stream_lds_bytes(const Geom& g, int threads);
 // Literal-draw slots the resident kernel precomputes per sample within an LDS budget.
 int train_rng_slots(int cpw, const Geom& g);
 

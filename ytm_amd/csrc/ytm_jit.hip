@@ -39,6 +39,7 @@ void append_value(std::string* s, double v) {
 const char* kernel_name(TrainKind kind) {
   switch (kind) {
     case TrainKind::kResident: return "ytm_jit_train_resident";
+    case TrainKind::kStream: return "ytm_jit_train_stream";
     case TrainKind::kGlobalVanilla: return "ytm_jit_train_global_vanilla";
     default: return "ytm_jit_train_global_conv";
   }
@@ -60,6 +61,9 @@ std::string kernel_source(const Geom& g, TrainKind kind, bool inject) {
   switch (kind) {
     case TrainKind::kResident:
       s += std::string("ytm::train_resident_body<") + inj + ">(a, ytm::kJitGeom);\n";
+      break;
+    case TrainKind::kStream:
+      s += "ytm::train_stream_body(a, ytm::kJitGeom);\n";
       break;
     case TrainKind::kGlobalVanilla:
       s += std::string("ytm::train_global_body<true, ") + inj + ">(a, ytm::kJitGeom);\n";

@@ -695,6 +695,8 @@ __global__ __launch_bounds__(kTrainThreads) void train_resident_kernel(TrainArgs
   train_resident_body<INJECT>(a, a.g);
 }
 
+__global__ __launch_bounds__(kTrainThreads) void train_stream_kernel(TrainArgs a) { train_stream_body(a, a.g); }
+
 // ========================================================================= launchers
 static int grid_for(int64_t items, int block) {
   int64_t g = (items + block - 1) / block;
@@ -1020,8 +1022,19 @@ size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g) {
          K * 4 + 3 * C * 4 + 6 * C * K * 4 + 2 * C * 4 + C * K * 4 + 2 * R * 4 + R * W * kPreGroups * 4 * 4;
 }
 
+size_t stream_lds_bytes(const Geom& g, int threads) {
+  // layout of train_stream_body: task masks [64][3] u64; planes [64][np][W]; weights [64][K]
+  // f32 and [K][64] i32; include counts, drop, patch weights, task clauses, zeros, stop
+  // selections [64] i32 each; targets ring [depth][K]; complemented samples [waves - 1][Wp]
+  const size_t C = kStreamClauses, K = (size_t)g.K, Wp = (size_t)((g.W + 3) & ~(int64_t)3);
+  return 3 * C * 8 + C * (size_t)g.np * (size_t)g.W * 4 + 2 * C * K * 4 + 6 * C * 4 + (size_t)kStreamDepth * K * 4 +
+         (size_t)(threads / kWave - 1) * Wp * 4;
+}
+
 static const void* train_fn(TrainKind kind, bool inject) {
   switch (kind) {
+    case TrainKind::kStream:
+      return (const void*)train_stream_kernel;
     case TrainKind::kResident:
       return inject ? (const void*)train_resident_kernel<true> : (const void*)train_resident_kernel<false>;
     case TrainKind::kGlobalVanilla:

@@ -1729,4 +1729,370 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   }
 }
 
+// ========================================================================= streaming
+// One-patch models, coalesced classes, counter stream, at most 64 clauses per workgroup
+// (one lane each).  A sample changes the clause state only when some class has an update
+// probability above zero: the update draw u lies in (0, 1] and a class updates only when
+// u <= prob (kernel.cu:508-529,573-575), so with prob <= 0 for every class no weight and no
+// TA state changes (the patch weights do, but nothing reads them during training).  Once a
+// model is trained, most samples are like that (config 2 after five epochs: 96%).
+//
+// So the workgroups stream: each evaluates the samples ahead of the one being consumed with
+// the current state and publishes their partial class sums (one flat row of K words per
+// sample, every workgroup adding (1 << 44) | partial), while wave 0 consumes the completed
+// rows in order.  A consumed sample whose classes all have prob <= 0 only commits its patch
+// weights; the rows already published for later samples stay exact because nothing
+// changed.  The first sample with some prob > 0 stops the stream in every workgroup (all
+// see the same sums): the workgroup takes that sample's feedback decisions and literal
+// updates (the same functions as the resident kernel), and streaming restarts at the next
+// sample on fresh rows, so the speculative rows published past the stop are never read.
+// The result is exactly the sequential one.
+//
+// Rows of a stream that starts at sample b with first row r0: row(s) = r0 + (s - b).  A
+// workgroup publishes a sample only while it is fewer than kStreamDepth samples ahead of
+// the one it consumes, so a stream that stops at sample j used rows below r0 + (j - b) +
+// kStreamDepth; the next stream starts at row r0 + (j + 1 - b) + kStreamDepth.  Every
+// workgroup derives the same rows from the same stops.
+struct StreamCtl {
+  int claim;    // next sample to evaluate
+  int consume;  // next sample to consume: every earlier sample of this stream is final
+  int stop;     // -1 while streaming; then the sample that needs feedback, or N
+  int abort;
+};
+
+__device__ __forceinline__ int lds_load(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_store(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom& g) {
+  extern __shared__ long long dyn_lds[];
+  __shared__ StreamCtl ctl;
+  __shared__ unsigned long long s_ring[kStreamDepth];  // selected clauses of in-flight samples
+  __shared__ long long s_S[64];                        // class sums + bias of the stop sample
+  __shared__ int s_ntask;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int nwv = blockDim.x / kWave;
+  const int G = gridDim.x, wg = blockIdx.x;
+  const int64_t c_begin = g.C * wg / G, c_end = g.C * (wg + 1) / G;
+  const int n_own = (int)(c_end - c_begin);  // <= kStreamClauses
+  const int64_t cw = (int64_t)g.np * g.W;
+  const int K = (int)g.K;
+  const int64_t Wp = (g.W + 3) & ~(int64_t)3;
+  constexpr int D = kStreamDepth;
+  // LDS (sizes in train_lds_bytes): task masks [64][3] u64; planes [64][np][W]; weights
+  // [64][K]; transposed integer weights [K][64]; include counts, drop, patch weights, task
+  // clauses, zeros, selections of the stop sample [64] each; targets ring [D][K];
+  // complemented samples [waves][Wp].
+  unsigned long long* s_task_m = (unsigned long long*)dyn_lds;
+  uint32_t* s_planes = (uint32_t*)(s_task_m + 3 * kStreamClauses);
+  float* s_w = (float*)(s_planes + (int64_t)kStreamClauses * cw);
+  int* s_wt = (int*)(s_w + kStreamClauses * K);
+  int* s_ninc = s_wt + K * kStreamClauses;
+  int* s_drop = s_ninc + kStreamClauses;
+  int* s_pw = s_drop + kStreamClauses;
+  int* s_task_idx = s_pw + kStreamClauses;
+  int* s_zero = s_task_idx + kStreamClauses;
+  int* s_selj = s_zero + kStreamClauses;
+  int32_t* s_yring = s_selj + kStreamClauses;
+  uint32_t* s_nx = (uint32_t*)(s_yring + D * K);
+  const bool exact_count = g.maxinc < g.L;
+  const int ks = (K + 15) & ~15;
+  unsigned long long my_updates = 0ull, my_evals = 0ull, my_stops = 0ull;
+  uint64_t wait_ticks = 0;
+  const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
+
+  for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) s_planes[j] = a.planes[c_begin * cw + j];
+  for (int64_t j = threadIdx.x; j < n_own * K; j += blockDim.x) {
+    const float w = a.weights[c_begin * K + j];
+    s_w[j] = w;
+    s_wt[(j % K) * kStreamClauses + j / K] = (int)w;
+  }
+  for (int j = threadIdx.x; j < kStreamClauses; j += blockDim.x) {
+    s_drop[j] = j < n_own ? a.drop[c_begin + j] == 1u : 1;
+    s_pw[j] = j < n_own ? a.patch_w[c_begin + j] : 0;
+    s_zero[j] = 0;
+  }
+  __syncthreads();
+  // include counts (or emptiness when MAX_INCLUDED_LITERALS >= L), one clause per wave
+  for (int idx = wave; idx < n_own; idx += nwv) {
+    const uint32_t* m = s_planes + idx * cw + (int64_t)(g.np - 1) * g.W;
+    int cnt = 0;
+    for (int64_t w = lane; w < g.W; w += kWave) cnt += __popc(m[w]);
+    cnt = wave_sum_i32(cnt);
+    if (lane == 0) s_ninc[idx] = exact_count ? cnt : (cnt > 0);
+  }
+
+  // Profile (a.profile, wave 0's view, summed into counters[4..7]): streaming, draining the
+  // evaluation waves after a stop, feedback decisions, literal updates.
+  const bool prof = a.profile && wave == 0;
+  uint64_t prof_acc[4] = {0, 0, 0, 0};
+  uint64_t prof_last = t_kernel;
+  int gen_start = 0;
+  int64_t row_base = 0;
+  // Lookahead at the start of a stream: twice the previous stream's length (2 to D), so that
+  // speculation stays shallow while stops are frequent and is deep as soon as they are rare.
+  int depth0 = 2;
+  while (gen_start < a.N) {
+    if (threadIdx.x == 0) {
+      ctl.claim = gen_start;
+      ctl.consume = gen_start;
+      ctl.stop = -1;
+      ctl.abort = 0;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // ---- consumer: rows in order, up to 64 / K at a time (lane = (row q, class k))
+      const int nq = K <= 32 ? kWave / K : 1;
+      const int q = lane / K, k = lane - (lane / K) * K;
+      const long long bias_k = (long long)a.bias[k];
+      int j = gen_start;
+      int stop = -1;
+      while (j < a.N) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        bool here = q < nq && j + q < a.N;  // this lane's (row, class) exists
+        unsigned long long v = 0;
+        int ncomp = 0;
+        for (unsigned polls = 1;; ++polls) {
+          bool ok = true;
+          if (here) {
+            v = __hip_atomic_load(&a.slots[(row_base + (j + q - gen_start)) * ks + k], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+            ok = ((v + (1ull << 43)) >> 44) == (unsigned long long)G;
+          }
+          // complete rows from j on: the first row with an incomplete word ends them
+          const unsigned long long bad = __ballot(here && !ok);
+          const int first_bad = bad ? (__ffsll((long long)bad) - 1) / K : nq;
+          const int avail = a.N - j < nq ? a.N - j : nq;
+          ncomp = first_bad < avail ? first_bad : avail;
+          if (ncomp > 0) break;
+          if ((polls & 15u) == 0u && lds_load(&ctl.abort)) break;  // an evaluation wave gave up
+          if ((polls & 15u) == 0u && __builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) {
+            if (lane == 0) {
+              lds_store(&ctl.abort, 1);
+              if (atomicCAS(a.err, 0, 1) == 0) {
+                a.err[1] = j;
+                a.err[2] = wg;
+                a.err[3] = (int)((v + (1ull << 43)) >> 44);
+              }
+            }
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        wait_ticks += __builtin_amdgcn_s_memrealtime() - t0;
+        if (ncomp == 0) break;  // aborted
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // the rows' LDS rings are written
+        // feedback possible in row q?  prob > 0 for some class (class_fb, kernel.cu:508-529)
+        const bool live = here && q < ncomp;
+        const long long S = (long long)(v - ((unsigned long long)G << 44)) + bias_k;
+        bool fb = false;
+        if (live) {
+          const int y = s_yring[((j + q) & (D - 1)) * K + k];
+          fb = class_fb(g, S, y).prob > 0.0;
+        }
+        const unsigned long long fbm = __ballot(fb);
+        const int qf = fbm ? (__ffsll((long long)fbm) - 1) / K : ncomp;  // first row with feedback
+        // patch weights of the rows before it (select_active, kernel.cu:305)
+        for (int r = 0; r < qf; ++r) {
+          const unsigned long long sm = s_ring[(j + r) & (D - 1)];
+          if (lane < n_own) s_pw[lane] += (int)((sm >> lane) & 1ull);
+        }
+        if (qf < ncomp) {
+          if (q == qf) s_S[k] = S;
+          stop = j + qf;
+          break;
+        }
+        j += ncomp;
+        if (lane == 0) lds_store(&ctl.consume, j);
+      }
+      if (lane == 0) lds_store(&ctl.stop, stop >= 0 ? stop : a.N);
+    } else {
+      // ---- evaluation: claim samples in order, evaluate with the current state, publish
+      uint32_t* nx = s_nx + (int64_t)(wave - 1) * Wp;
+      const bool own = lane < n_own;
+      const uint32_t* m = s_planes + (int64_t)(own ? lane : 0) * cw + (int64_t)(g.np - 1) * g.W;
+      for (;;) {
+        if (lds_load(&ctl.stop) >= 0) break;
+        int s = 0;
+        if (lane == 0) s = atomicAdd(&ctl.claim, 1);
+        s = lane_value(s, 0);
+        if (s >= a.N) break;
+        // at most min(D, depth0 + consumed samples of this stream) ahead of the consumer
+        bool skip = false;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        for (unsigned spins = 1;; ++spins) {
+          const int cons = lds_load(&ctl.consume);
+          const int ahead = depth0 + (cons - gen_start) < D ? depth0 + (cons - gen_start) : D;
+          if (s < cons + ahead) break;
+          if (lds_load(&ctl.stop) >= 0) {  // stopped before s: s is past the stop sample
+            skip = true;
+            break;
+          }
+          if ((spins & 15u) == 0u && __builtin_amdgcn_s_memrealtime() - t0 > 2 * kWaitTicks) {
+            if (lane == 0) {
+              lds_store(&ctl.abort, 1);
+              if (atomicCAS(a.err, 0, 1) == 0) {
+                a.err[1] = s;
+                a.err[2] = wg;
+                a.err[3] = -1;  // an evaluation wave, not the class-sum wait
+              }
+            }
+            skip = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        if (skip) break;
+        // the sample's complemented words (broadcast reads below) and its targets
+        for (int64_t w = lane; w < g.W; w += kWave) nx[w] = ~a.X[(int64_t)s * g.W + w];
+        if (lane < K) s_yring[(s & (D - 1)) * K + lane] = a.Y[(int64_t)s * K + lane];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        // fast_eval (kernel.cu:255-282): an empty clause fires in training
+        uint32_t bad = 0u;
+        for (int64_t w = 0; w < g.W; ++w) bad |= m[w] & nx[w];
+        const bool fire = own && s_drop[lane] == 0 && (s_ninc[lane] == 0 || bad == 0u);
+        // a stop set meanwhile lies before s: its row will not be read
+        if (lds_load(&ctl.stop) >= 0) break;
+        // select_active (kernel.cu:285-316) with one patch: selected when the rank-1 draw is
+        // below 1.0f / 1
+        bool sel = false;
+        if (__any(fire)) {
+          const U4 z = site_words(a.seed, a.step0 + (uint64_t)s, (uint32_t)(c_begin + (own ? lane : 0)), TAG_SEL, 0u);
+          sel = fire && uniform_from_word(z.x) < 1.0f;
+        }
+        const unsigned long long smask = __ballot(sel);
+        int mine = 0;
+        if (smask)
+          for (int kk = 0; kk < K; ++kk) {
+            const int p = wave_sum_i32(sel ? s_wt[kk * kStreamClauses + lane] : 0);
+            if (lane == kk) mine = p;
+          }
+        if (lane == 0) s_ring[s & (D - 1)] = smask;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // ring and targets before the publish
+        if (lane < K)
+          __hip_atomic_fetch_add(&a.slots[(row_base + (s - gen_start)) * ks + lane],
+                                 (1ull << 44) + (unsigned long long)(long long)mine, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        ++my_evals;
+      }
+    }
+    if (prof) {
+      const uint64_t now = __builtin_amdgcn_s_memrealtime();
+      prof_acc[0] += now - prof_last;
+      prof_last = now;
+    }
+    __syncthreads();
+    if (prof) {
+      const uint64_t now = __builtin_amdgcn_s_memrealtime();
+      prof_acc[1] += now - prof_last;
+      prof_last = now;
+    }
+    const int stop = ctl.stop;
+    if (ctl.abort) break;
+    if (stop >= a.N) break;
+
+    // ---- feedback of sample `stop` (clause_update, kernel.cu:531-613), whole workgroup
+    const uint64_t t = a.step0 + (uint64_t)stop;
+    const unsigned long long selm = s_ring[stop & (D - 1)];
+    if (threadIdx.x < kStreamClauses) s_selj[threadIdx.x] = ((selm >> threadIdx.x) & 1ull) ? 0 : -1;
+    if (threadIdx.x == 0) s_ntask = 0;
+    ++my_stops;
+    __syncthreads();
+    {
+      const int kn = K, cpp = kWave / kn;
+      const int jc = lane / kn, kk = lane - jc * kn;
+      const unsigned long long seg = kn == kWave ? ~0ull : ((1ull << kn) - 1ull);
+      const ClassPrep cp = class_prep(g, s_yring[(stop & (D - 1)) * K + (kk < K ? kk : 0)]);
+      const ClassTest ct = class_test(g, s_S[kk < K ? kk : 0], cp);
+      for (int base = wave * cpp; base < n_own; base += nwv * cpp) {
+        const int idx = base + jc;
+        const bool valid = jc < cpp && idx < n_own;
+        const int ix = valid ? idx : base;  // idle lanes read a valid clause and discard it
+        const int64_t c = c_begin + ix;
+        const float w0 = s_w[ix * K + kk];
+        const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)kk);
+        const PairOps po = decide_pair<false>(g, nullptr, c, kk, valid && s_drop[ix] == 0, s_selj[ix], s_ninc[ix],
+                                              ct.tgt, ct.num, ct.den, w0, uniform_from_word(z.x),
+                                              uniform_from_word(z.y));
+        if (valid && (po.t1a || po.t2)) {
+          s_w[ix * K + kk] = po.w_new;
+          s_wt[kk * kStreamClauses + ix] = (int)po.w_new;
+        }
+        const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
+        if ((b1a | b1b | bt2) == 0ull) continue;
+        const int sh = jc * kn;
+        const unsigned long long m1a = valid ? (b1a >> sh) & seg : 0ull;
+        const unsigned long long m1b = valid ? (b1b >> sh) & seg : 0ull;
+        const unsigned long long m2 = valid ? (bt2 >> sh) & seg : 0ull;
+        const bool leader = (m1a | m1b | m2) != 0ull && kk == 0;
+        my_updates += (unsigned long long)__popcll(__ballot(leader));
+        if (leader) {
+          const int tk = atomicAdd(&s_ntask, 1);
+          s_task_idx[tk] = ix;
+          s_task_m[tk * 3 + 0] = m1a;
+          s_task_m[tk * 3 + 1] = m1b;
+          s_task_m[tk * 3 + 2] = m2;
+        }
+      }
+    }
+    __syncthreads();
+    if (prof) {
+      const uint64_t now = __builtin_amdgcn_s_memrealtime();
+      prof_acc[2] += now - prof_last;
+      prof_last = now;
+    }
+    const int ntask = s_ntask;
+    const uint32_t* xe = a.X + (int64_t)stop * g.W;  // the sample's words, for the literal updates
+    if (g.W <= 32) {
+      const int per = tasks_per_wave(g, ntask, nwv);
+      for (int tk0 = wave * per; tk0 < ntask; tk0 += nwv * per)
+        apply_tasks<false>(a, g, nullptr, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_zero, s_selj,
+                           s_planes, xe, nullptr, 0);
+    } else {
+      for (int tk = wave; tk < ntask; tk += nwv) {
+        const int idx = s_task_idx[tk];
+        const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
+        apply_ops<false>(a, g, nullptr, c_begin + idx, t, s_selj[idx], ops, s_planes + idx * cw, xe, nullptr);
+      }
+    }
+    __syncthreads();
+    for (int tk = wave; tk < ntask; tk += nwv) {  // include counts of the updated clauses
+      const int idx = s_task_idx[tk];
+      const uint32_t* mt = s_planes + idx * cw + (int64_t)(g.np - 1) * g.W;
+      int cnt = 0;
+      for (int64_t w = lane; w < g.W; w += kWave) cnt += __popc(mt[w]);
+      cnt = wave_sum_i32(cnt);
+      if (lane == 0) s_ninc[idx] = exact_count ? cnt : (cnt > 0);
+    }
+    if (wave == 0 && lane < n_own) s_pw[lane] += (int)((selm >> lane) & 1ull);  // the stop sample's
+    row_base += (int64_t)(stop + 1 - gen_start) + D;
+    depth0 = 2 * (stop + 1 - gen_start) < D ? (2 * (stop + 1 - gen_start) > 2 ? 2 * (stop + 1 - gen_start) : 2) : D;
+    gen_start = stop + 1;
+    __syncthreads();
+    if (prof) {
+      const uint64_t now = __builtin_amdgcn_s_memrealtime();
+      prof_acc[3] += now - prof_last;
+      prof_last = now;
+    }
+  }
+  __syncthreads();
+  for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) a.planes[c_begin * cw + j] = s_planes[j];
+  for (int64_t j = threadIdx.x; j < n_own * K; j += blockDim.x) a.weights[c_begin * K + j] = s_w[j];
+  for (int j = threadIdx.x; j < n_own; j += blockDim.x) a.patch_w[c_begin + j] = s_pw[j];
+  if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
+  if (lane == 0 && my_evals) atomicAdd(&a.counters[13], my_evals);
+  if (threadIdx.x == 0) {
+    atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
+    atomicAdd(&a.counters[2], (unsigned long long)(__builtin_amdgcn_s_memrealtime() - t_kernel));
+    if (wg == 0) atomicAdd(&a.counters[12], my_stops);
+    if (prof)
+      for (int j = 0; j < 4; ++j) atomicAdd(&a.counters[4 + j], (unsigned long long)prof_acc[j]);
+  }
+}
+
 }  // namespace ytm

@@ -72,6 +72,13 @@ __host__ __device__ constexpr bool literal_major_lds(const Geom& g) {
   return literal_major(g) && g.L * ((g.P + 31) / 32) * 4 <= 120 * 1024;
 }
 
+// Streaming training kernel (train_stream_body): in-flight samples per workgroup (a power
+// of two), most clauses per workgroup (one lane each), and the class-sum rows a launch of n
+// samples may use at most (every sample a stop).
+constexpr int kStreamDepth = 32;
+constexpr int kStreamClauses = 64;
+__host__ __device__ constexpr int64_t stream_rows(int64_t n) { return n * (kStreamDepth + 1); }
+
 struct TrainArgs {
   uint32_t* planes;          // [C][np][W]
   float* weights;            // [C][K]
@@ -84,7 +91,8 @@ struct TrainArgs {
   const float* inject;       // [N][inject_block] or nullptr
   const float* inv_rank;     // [P + 1], inv_rank[r] = 1.0f / r
   unsigned long long* slots; // [N][slot_stride], zero on entry
-  unsigned long long* counters;  // [0] updated clauses, [1] wait ticks, [2] kernel ticks, [4..11] phases
+  unsigned long long* counters;  // [0] updated clauses, [1] wait ticks, [2] kernel ticks, [4..11] phases,
+                                 // [12] feedback samples, [13] evaluations (streaming kernel)
   int* err;                  // {1, sample, workgroup, count} when a bounded wait expires
   int64_t inject_block;
   uint64_t step0;
