@@ -1,17 +1,20 @@
 """Benchmark of the YTM Tsetlin Machine hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-extra] [--no-cpu]
 
 A step is one training epoch (one fit() pass over the whole training set, samples in
-order, data resident in HBM).  W untimed epochs, then K timed epochs; then inference
-over the test set.  Prints ONE JSON line on stdout.  The default workload is
-configuration 2 of BASELINE.json (MNIST-shaped, 2000 clauses, 10 classes, 49 words).
+order, data resident in HBM).  W untimed epochs, then K timed epochs of the headline
+configuration (BASELINE.json's config 2 by default: MNIST-shaped, 2000 clauses, 10 classes,
+49 words), then inference over its test set.  The other four configurations follow at their
+full sizes under "configs" (config 1: one untimed epoch, then its 10 epochs; configs 3-5: one untimed and two timed
+epochs), each with the C oracle's CPU rate beside it.  Prints ONE JSON line on stdout.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 from pathlib import Path
@@ -24,13 +27,16 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 # VALU 32-bit lane-ops per second: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz (MI355X).
 VALU_PEAK_T = 256 * 4 * 16 * 2.4e9 / 1e12
+# Epochs of the configurations run after the headline one: (untimed, timed).
+EXTRA_EPOCHS = {1: (1, 10), 2: (1, 3), 3: (1, 2), 4: (1, 2), 5: (1, 2)}
+KIND_NAMES = {0: "resident", 1: "global one-patch", 2: "global several-patch", 3: "streaming"}
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def train_bytes_per_launch(tm, samples: int, updates: int) -> float:
+def train_bytes(tm, samples: int, updates: int) -> float:
     """Algorithmic HBM bytes of training: every TA state read once at 2 B, every weight at
     4 B, per sample; clauses that ran a feedback branch write their TA row and weights
     back; each sample's literals are read once:  B = (N*C + U)(2L + 4K) + N*4*P*W."""
@@ -55,9 +61,22 @@ def load_traffic(config: int):
     if not path.exists():
         return None
     try:
-        return float(json.loads(path.read_text())["bytes_per_launch"])
+        d = json.loads(path.read_text())
+        return {"bytes_per_launch": float(d["bytes_per_launch"]), "kernel": d.get("kernel")}
     except (KeyError, ValueError):
         return None
+
+
+def cpu_info() -> dict:
+    model = platform.processor() or "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
 
 
 def copy_calibration(mib: int) -> None:
@@ -83,103 +102,103 @@ def copy_calibration(mib: int) -> None:
     log(f"[bench] copy calibration: {mib} MiB device-to-device")
 
 
-def cpu_baseline(encX, y, kw, budget_s: float):
-    """The C oracle (a CPU restatement of the reference semantics) training on a bounded
-    prefix of the same workload, from the same initial state, on this host's cores."""
+def encode_in_chunks(tm, make_chunk, n: int, chunk: int) -> np.ndarray:
+    """Encoded samples (n, P, W) on the host, the raw inputs generated and encoded chunk by
+    chunk (the full raw array of config 4 is 4.9 GB of uint32)."""
+    out = np.empty((n, tm.number_of_patches, tm.number_of_literal_chunks), dtype=np.uint32)
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        out[s:e] = tm.encode(make_chunk(s, e))
+    return out
+
+
+def cpu_baseline(cfg: int, kw: dict, encX, y, encXt, budget_s: float) -> dict:
+    """The C oracle (a CPU restatement of the reference semantics, oracle/ytm_oracle.c)
+    training on a prefix of the same workload from the same initial state, then scoring a
+    prefix of the test set, on this host's cores (OpenMP)."""
     from oracle import oracle as orc
 
-    threads = min(16, os.cpu_count() or 1)
+    info = cpu_info()
+    threads = min(16, info["nproc"] or 1)
     orc.set_threads(threads)
     ref = orc.OracleTM(kw["number_of_clauses_per_class"], kw["T"], kw["s"], kw["dim"], kw["n_classes"],
                        patch_dim=kw.get("patch_dim"), seed=kw["seed"])
     encY = ref.encode_y_multiclass(y)
-    # consecutive chunks of the epoch (the oracle's step counter carries across calls, so
-    # this is the same computation as one fit over the prefix) until the budget is spent
+    # consecutive chunks of epoch 1 (the oracle's step counter carries across calls, so this
+    # is the same computation as one fit over the prefix) until the budget is spent
     t0 = time.perf_counter()
-    n, chunk = 0, 32
+    n, chunk = 0, 8
     while n < encX.shape[0] and time.perf_counter() - t0 < budget_s:
         m = min(chunk, encX.shape[0] - n)
         ref.fit_encoded(encX[n:n + m], encY[n:n + m])
         n += m
         chunk = min(2 * chunk, 2048)
-    total = time.perf_counter() - t0
+    train_s = time.perf_counter() - t0
+    nt = min(encXt.shape[0], 1000)
+    t1 = time.perf_counter()
+    ref.score(encXt[:nt])
+    infer_s = time.perf_counter() - t1
     return {
-        "value": n / total,
+        "value": round(n / train_s, 1),
         "unit": "train samples/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"first {n} training samples of epoch 1 (fresh model, same seed), "
-                  f"{total:.1f} s on {threads} threads; C oracle oracle/ytm_oracle.c",
+        "infer_samples_per_s": round(nt / infer_s, 1),
+        "nproc": info["nproc"],
+        "cpu_model": info["cpu_model"],
+        "sample": f"config {cfg}: first {n} training samples of epoch 1 (fresh model, same seed) in {train_s:.1f} s, "
+                  f"then {nt} test samples scored, on {threads} OpenMP threads of {info['nproc']}; "
+                  f"C oracle oracle/ytm_oracle.c",
     }
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--n-train", type=int, default=None)
-    ap.add_argument("--n-test", type=int, default=None)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="first copy MIB MiB device-to-device (counter calibration under rocprofv3 --pmc)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the training path is "
-              "single-GPU by design, see DESIGN.md for how it would shard.", file=sys.stderr)
-        return 2
-
+def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=None, n_test=None) -> dict:
     import workloads
     from ytm_amd import MultiClassTM
 
-    if args.copy_calibration:
-        copy_calibration(args.copy_calibration)
-
-    cfg = args.config
     t0 = time.perf_counter()
-    X, y, Xt, yt, kw = workloads.make(cfg, args.n_train, args.n_test)
-    kw["seed"] = workloads.MODEL_SEED
-    log(f"[bench] config {cfg} data {X.shape} / {Xt.shape} generated in {time.perf_counter() - t0:.1f}s")
+    c = workloads.CONFIGS[cfg]
+    kw = dict(c["model"], seed=workloads.MODEL_SEED)
     tm = MultiClassTM(**kw)
-    encX = tm.encode(X)
-    enc_ms = tm.stats()["last_encode_kernel_ms"]
-    encXt = tm.encode(Xt)
+    if cfg == 4 and n_train is None and n_test is None:
+        # the values of workloads.make(4), generated and encoded in chunks
+        gen = workloads.CifarStream(c["n_train"], c["n_test"])
+        encX = encode_in_chunks(tm, gen.train_rows, c["n_train"], 2048)
+        enc_ms = tm.stats()["last_encode_kernel_ms"]
+        encXt = encode_in_chunks(tm, gen.test_rows, c["n_test"], 2048)
+        y, yt = gen.y, gen.yt
+    else:
+        X, y, Xt, yt, _ = workloads.make(cfg, n_train, n_test)
+        encX = tm.encode(X)
+        enc_ms = tm.stats()["last_encode_kernel_ms"]
+        encXt = tm.encode(Xt)
+        del X, Xt
     dtrain = tm.device_data(encX, y, is_X_encoded=True)
     dtest = tm.device_data(encXt, is_X_encoded=True)
     N, Nt = encX.shape[0], encXt.shape[0]
+    log(f"[bench] config {cfg}: {N} / {Nt} samples generated, encoded and resident in {time.perf_counter() - t0:.1f}s")
 
-    epoch1 = None
-    for w in range(args.warmup):
+    epochs = []
+    for e in range(warmup + steps):
         t = time.perf_counter()
         tm.fit_device(dtrain)
+        wall = time.perf_counter() - t
         st = tm.stats()
-        log(f"[bench] warmup epoch {w + 1}: {time.perf_counter() - t:.3f}s kernel {st['last_fit_kernel_ms']:.1f}ms "
-            f"updates {st['last_fit_updates']}")
-        if w == 0:
-            epoch1 = N / (st["last_fit_kernel_ms"] / 1e3)
-
-    walls, kern, byts, launches, upd = [], [], [], 0, 0
-    for s in range(args.steps):
-        t = time.perf_counter()
-        tm.fit_device(dtrain)
-        walls.append(time.perf_counter() - t)
-        st = tm.stats()
-        kern.append(st["last_fit_kernel_ms"])
-        launches += st["last_fit_launches"]
-        upd += st["last_fit_updates"]
-        byts.append(train_bytes_per_launch(tm, N, st["last_fit_updates"]))
-        log(f"[bench] step {s + 1}: wall {walls[-1]:.3f}s kernel {kern[-1]:.1f}ms updates {st['last_fit_updates']} "
-            f"({st['last_fit_updates'] / N:.1f}/sample) workgroups {st['train_workgroups']} "
-            f"kind {st['train_kind']} wait {st['last_fit_wait_frac']:.3f} "
-            f"feedback samples {st['last_fit_feedback_samples']} evaluations {st['last_fit_evaluations']}")
+        ep = dict(wall_s=wall, kernel_ms=st["last_fit_kernel_ms"], launches=st["last_fit_launches"],
+                  updates=st["last_fit_updates"], feedback=st["last_fit_feedback_samples"],
+                  evals=st["last_fit_evaluations"], wait=st["last_fit_wait_frac"], kind=st["train_kind"],
+                  wgs=st["train_workgroups"], phase=st["last_fit_phase_us"])
+        epochs.append(ep)
+        log(f"[bench] config {cfg} epoch {e + 1}{' (timed)' if e >= warmup else ''}: wall {wall:.3f}s "
+            f"kernel {ep['kernel_ms']:.1f}ms updates {ep['updates']} ({ep['updates'] / N:.2f}/sample) "
+            f"feedback samples {ep['feedback']} evaluations {ep['evals']} workgroups {ep['wgs']} "
+            f"kernel {KIND_NAMES.get(ep['kind'], ep['kind'])} wait {ep['wait']:.3f}")
         if os.environ.get("YTM_TRAIN_PROFILE"):
             names = {0: ("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier", "step1-slowest-wave"),
                      3: ("stream", "drain", "decide", "apply")}.get(
-                         st["train_kind"], ("A", "barrier", "exchange", "barrier", "D", "barrier"))
-            log("[bench]   phase us/sample (wave 0): "
-                + " ".join(f"{n} {v:.2f}" for n, v in zip(names, st["last_fit_phase_us"])))
+                         ep["kind"], ("A", "barrier", "exchange", "barrier", "D", "barrier"))
+            log("[bench]   phase us/sample (wave 0): " + " ".join(f"{n} {v:.2f}" for n, v in zip(names, ep["phase"])))
+    timed = epochs[warmup:]
 
     # inference over the test set (resident), best of 3 after one warm call
     cs = tm.score_device(dtest)
@@ -190,61 +209,52 @@ def main() -> int:
         inf.append((time.perf_counter() - t, tm.stats()["last_score_kernel_ms"]))
     inf_wall, inf_kern = min(inf)
     acc = float((np.argmax(cs, axis=1) == yt).mean())
-    log(f"[bench] test accuracy after {args.warmup + args.steps} epochs: {acc:.4f}")
+    dtrain.release()
+    dtest.release()
 
-    # PCIe-inclusive rate: one more epoch through fit() from host arrays (upload + train),
-    # after the timed region and the inference above
-    t = time.perf_counter()
-    tm.fit(encX, y, is_X_encoded=True)
-    host_wall = time.perf_counter() - t
-
-    total_wall = sum(walls)
-    value = N * args.steps / total_wall
-    avg_launch_s = sum(kern) / 1e3 / max(1, launches)
-    bytes_per_launch = sum(byts) / max(1, launches)
-    achieved = bytes_per_launch / avg_launch_s / 1e9
-    out = {
-        "metric": "train & infer samples/sec on 1 MI355X; % of HBM-bandwidth roofline",
-        "value": round(value, 1),
-        "unit": "train samples/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(1e3 * total_wall / args.steps, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "u32",
-        "data": "synthetic (seeded generator, workloads.py)",
-        "config": {
-            "workload": workloads.CONFIGS[cfg]["name"],
-            "bench_config": cfg,
-            "train_samples": N,
-            "test_samples": Nt,
-            "clauses": tm.number_of_clauses,
-            "classes": tm.number_of_outputs,
-            "literals": tm.number_of_literals,
-            "literal_words": tm.number_of_literal_chunks,
-            "patches": tm.number_of_patches,
-            "T": kw["T"],
-            "s": kw["s"],
-            "step": "one training epoch (fit over all training samples, in order)",
-        },
+    kern_s = sum(e["kernel_ms"] for e in timed) / 1e3
+    wall_s = sum(e["wall_s"] for e in timed)
+    launches = sum(e["launches"] for e in timed)
+    upd = sum(e["updates"] for e in timed)
+    byts = sum(train_bytes(tm, N, e["updates"]) for e in timed)
+    achieved = byts / kern_s / 1e9  # bytes per launch / average launch time
+    last = timed[-1]
+    res = {
+        "workload": c["name"],
+        "train_samples": N,
+        "test_samples": Nt,
+        "clauses": tm.number_of_clauses,
+        "classes": tm.number_of_outputs,
+        "literal_words": tm.number_of_literal_chunks,
+        "patches": tm.number_of_patches,
+        "epochs": {"untimed": warmup, "timed": steps},
+        "train_samples_per_s": round(N * steps / wall_s, 1),
+        "train_kernel_samples_per_s": round(N * steps / kern_s, 1),
+        "epoch1_train_kernel_samples_per_s": round(N / (epochs[0]["kernel_ms"] / 1e3), 1),
+        "last_epoch_train_kernel_samples_per_s": round(N / (last["kernel_ms"] / 1e3), 1),
         "infer_samples_per_s": round(Nt / inf_wall, 1),
         "infer_kernel_samples_per_s": round(Nt / (inf_kern / 1e3), 1),
-        "train_kernel_samples_per_s": round(N * args.steps / (sum(kern) / 1e3), 1),
-        "train_samples_per_s_from_host_buffers": round(N / host_wall, 1),
-        "epoch1_train_kernel_samples_per_s": round(epoch1, 1) if epoch1 else None,
         "encode_samples_per_s": round(N / (enc_ms / 1e3), 1) if enc_ms else None,
-        "updates_per_sample": round(upd / (N * args.steps), 2),
+        "updates_per_sample": round(upd / (N * steps), 3),
         "test_accuracy": round(acc, 4),
+        "train_kernel": KIND_NAMES.get(last["kind"], last["kind"]),
+        "train_workgroups": last["wgs"],
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": load_traffic(cfg),
+            "traffic": None,
+            "U_s": round(upd / (N * steps), 3),
+            "bytes_per_launch": round(byts / max(1, launches), 1),
+        },
+        # what actually binds the training kernel: the share of its time spent waiting for
+        # class sums, and how many samples needed a feedback pass
+        "binding": {
+            "class_sum_wait_fraction": round(sum(e["wait"] for e in timed) / len(timed), 4),
+            "feedback_sample_fraction": round(sum(e["feedback"] for e in timed) / (N * steps), 4),
+            "evaluations_per_sample": round(sum(e["evals"] for e in timed) / (N * steps), 3),
         },
         "infer_roofline": {
             "bound": "valu",
@@ -254,14 +264,83 @@ def main() -> int:
             "frac": round(infer_word_ands(tm, Nt) / (inf_kern / 1e3) / 1e12 / VALU_PEAK_T, 4),
             "hbm_gbs": round(infer_bytes(tm, Nt) / (inf_kern / 1e3) / 1e9, 2),
         },
-        "cpu_baseline": None,
+        "_ms_per_step": 1e3 * wall_s / steps,
     }
-    out["train_wait_fraction"] = round(tm.stats()["last_fit_wait_frac"], 4)
-    dtrain.release()
-    dtest.release()
+    traffic = load_traffic(cfg)
+    if traffic:
+        res["roofline"]["traffic"] = traffic["bytes_per_launch"]
+        res["roofline"]["traffic_kernel"] = traffic["kernel"]
     tm.release()
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(encX, y, kw, args.cpu_seconds)
+    if cpu_seconds > 0:
+        res["cpu_baseline"] = cpu_baseline(cfg, kw, encX, y, encXt, cpu_seconds)
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--n-train", type=int, default=None)
+    ap.add_argument("--n-test", type=int, default=None)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-oracle budget per configuration")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline configuration")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB device-to-device (counter calibration under rocprofv3 --pmc)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the training path is "
+              "single-GPU by design, see DESIGN.md for how it would shard.", file=sys.stderr)
+        return 2
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+
+    cpu = 0.0 if args.no_cpu else args.cpu_seconds
+    cfg = args.config
+    head = run_config(cfg, args.warmup, args.steps, cpu, args.n_train, args.n_test)
+    configs = {str(cfg): head}
+    if not args.no_extra:
+        for other in (1, 2, 3, 4, 5):
+            if other != cfg:
+                w, s = EXTRA_EPOCHS[other]
+                configs[str(other)] = run_config(other, w, s, cpu)
+
+    import workloads
+
+    kw = workloads.CONFIGS[cfg]["model"]
+    out = {
+        "metric": "train & infer samples/sec on 1 MI355X; % of HBM-bandwidth roofline",
+        "value": head["train_samples_per_s"],
+        "unit": "train samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["_ms_per_step"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic (seeded generators, workloads.py)",
+        "config": {
+            "workload": head["workload"],
+            "bench_config": cfg,
+            "train_samples": head["train_samples"],
+            "test_samples": head["test_samples"],
+            "clauses": head["clauses"],
+            "classes": head["classes"],
+            "literal_words": head["literal_words"],
+            "patches": head["patches"],
+            "T": kw["T"],
+            "s": kw["s"],
+            "step": "one training epoch (fit over all training samples, in order)",
+        },
+        "infer_samples_per_s": head["infer_samples_per_s"],
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "configs": {k: {kk: vv for kk, vv in v.items() if not kk.startswith("_")} for k, v in configs.items()},
+    }
     print(json.dumps(out), flush=True)
     return 0
 

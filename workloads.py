@@ -62,17 +62,27 @@ def _mnist_shaped(rng, n_train, n_test):
     return X, y, Xt, yt
 
 
-def _cifar_images(rng, means, n):
+def _cifar_rows(rng, means, labels):
     # thermometer j = 0..7: x >= (j+1)*255/9, layout [y][x][channel*8 + j]
     # (the closed form of src/tm_utils/binarizer.py:11,19)
-    y = rng.integers(0, means.shape[0], n)
-    img = np.clip(means[y] + rng.normal(0.0, 32.0, (n, 32, 32, 3)), 0, 255).astype(np.uint8)
+    n = labels.shape[0]
     thr = (np.arange(1, 9) * 255.0 / 9.0)
-    bits = img[..., None] >= thr  # (n, 32, 32, 3, 8)
-    return bits.reshape(n, 32 * 32 * 24).astype(np.uint32), y.astype(np.uint32)
+    img = np.clip(means[labels] + rng.normal(0.0, 32.0, (n, 32, 32, 3)), 0, 255).astype(np.uint8)
+    return (img[..., None] >= thr).reshape(n, 32 * 32 * 24).astype(np.uint32)  # (n, 32, 32, 3, 8)
 
 
-def _cifar_shaped(rng, n_train, n_test):
+def _cifar_images(rng, means, n, chunk=1024):
+    # The noise is drawn chunk by chunk, which gives the same values as one draw of the whole
+    # (n, 32, 32, 3) array while the temporaries stay in cache.
+    y = rng.integers(0, means.shape[0], n)
+    X = np.empty((n, 32 * 32 * 24), dtype=np.uint32)
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        X[s:e] = _cifar_rows(rng, means, y[s:e])
+    return X, y.astype(np.uint32)
+
+
+def _cifar_means(rng):
     from scipy.ndimage import gaussian_filter
 
     means = np.empty((10, 32, 32, 3))
@@ -80,9 +90,45 @@ def _cifar_shaped(rng, n_train, n_test):
         for ch in range(3):
             f = gaussian_filter(rng.standard_normal((32, 32)), 4.0)
             means[k, :, :, ch] = 255.0 * (f - f.min()) / (f.max() - f.min())
+    return means
+
+
+def _cifar_shaped(rng, n_train, n_test):
+    means = _cifar_means(rng)
     X, y = _cifar_images(rng, means, n_train)
     Xt, yt = _cifar_images(rng, means, n_test)
     return X, y, Xt, yt
+
+
+class CifarStream:
+    """Configuration 4's samples (the values of make(4, n_train, n_test)) generated on demand
+    in consecutive row ranges, training rows first, then test rows, so that the 4.9 GB of
+    raw uint32 training inputs never exist at once.  Labels: .y now, .yt once the test rows
+    are started."""
+
+    def __init__(self, n_train, n_test, seed=None):
+        self._rng = np.random.default_rng(DATA_SEED + 4 if seed is None else seed)
+        self._means = _cifar_means(self._rng)
+        self.n_train, self.n_test = n_train, n_test
+        self._y = self._rng.integers(0, 10, n_train)
+        self.y = self._y.astype(np.uint32)
+        self._yt = None
+        self.yt = None
+        self._pos = 0  # rows generated so far (training, then test)
+
+    def train_rows(self, s, e):
+        assert s == self._pos and e <= self.n_train, "rows must be generated in order"
+        self._pos = e
+        return _cifar_rows(self._rng, self._means, self._y[s:e])
+
+    def test_rows(self, s, e):
+        if self._yt is None:
+            assert self._pos == self.n_train, "the training rows come first"
+            self._yt = self._rng.integers(0, 10, self.n_test)
+            self.yt = self._yt.astype(np.uint32)
+        assert s == self._pos - self.n_train and e <= self.n_test, "rows must be generated in order"
+        self._pos = self.n_train + e
+        return _cifar_rows(self._rng, self._means, self._yt[s:e])
 
 
 def _docs(rng, probs, n, length=150):
