@@ -198,6 +198,9 @@ def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=No
                      3: ("stream", "drain", "decide", "apply")}.get(
                          ep["kind"], ("A", "barrier", "exchange", "barrier", "D", "barrier"))
             log("[bench]   phase us/sample (wave 0): " + " ".join(f"{n} {v:.2f}" for n, v in zip(names, ep["phase"])))
+            if ep["kind"] == 3 and ep["feedback"]:
+                log("[bench]   per stop, us: " + " ".join(f"{n} {v * N / ep['feedback']:.2f}"
+                                                       for n, v in zip(names[1:], ep["phase"][1:4])))
     timed = epochs[warmup:]
 
     # inference over the test set (resident), best of 3 after one warm call

@@ -322,6 +322,114 @@ __device__ __forceinline__ uint32_t firing_from_mask(const Geom& g, const uint32
   return acc;
 }
 
+// ---------------------------------------------------------------- lane groups
+// Groups of S lanes (S = 16 or 32: one DPP row or two) that each take their own clause.
+// Inclusive scan within each group (DPP row shifts; for S = 32 row_bcast:15 carries row 0
+// into row 1 and row 2 into row 3).  Call with every lane active.
+template <int S>
+__device__ __forceinline__ int group_scan_add(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr1, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr2, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr4, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr8, 0xf, 0xf, false);
+  if (S == 32) v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast15, 0xa, 0xf, false);
+  return v;
+}
+
+// Value of lane src (any lane; every lane active).
+__device__ __forceinline__ int lane_from(int v, int src) { return __builtin_amdgcn_ds_bpermute(4 * src, v); }
+
+// Phase A of up to 64 / S clauses of a model with several patches at once, one per group of
+// S lanes (S = 16 or 32, at least ceil(P/32)).  The calling lane's group takes clause c with
+// the literal list `list` (n literals, padded to a multiple of 8) when valid, else nothing.
+// Each group's result is eval_select_lm's for its clause: the firing bitmap over all patches
+// is the AND of the listed literals' bitsets in the literal-major sample xt (fast_eval,
+// kernel.cu:255-282; an empty clause fires on every patch), then the reservoir choice of the
+// firing patch (select_active, kernel.cu:285-316) from the same draws (rank r: site
+// (t, c, SEL, (r-1)/4), word (r-1)%4): a pass tests each open group's next 4*S ranks from the
+// top, and a group closes at its first hit.  Returns the group's selected patch or -1, the
+// same in every lane of the group.
+template <bool INJECT, int S>
+__device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const float* inj, uint64_t t, int64_t c,
+                                    bool valid, const uint16_t* list, int n, const uint32_t* xt, bool dropped) {
+  const int lane = lane_id();
+  const int j = lane & (S - 1);
+  const int gbase = lane - j;
+  const uint32_t gmask = S == 32 ? 0xFFFFFFFFu : ((1u << S) - 1u);
+  const int PW = (int)((g.P + 31) / 32);
+  const bool live = valid && !dropped;
+  // firing bitmap: lane j < PW of the group keeps patches [32j, 32j + 32)
+  uint32_t acc = (live && j < PW) ? ((j == PW - 1 && (g.P & 31)) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu) : 0u;
+  const int nn = live ? n : 0;
+  const int nmax = wave_max_i32(nn);
+  const uint32_t jl = (uint32_t)(j < PW ? j : 0);
+  for (int s0 = 0; s0 < nmax; s0 += 8) {
+    if (s0 < nn) {
+      const uint2 q0 = *(const uint2*)(list + s0), q1 = *(const uint2*)(list + s0 + 4);
+      const uint32_t w8[4] = {q0.x, q0.y, q1.x, q1.y};
+      uint32_t v = 0xFFFFFFFFu;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + jl];
+        v &= xt[(w8[u] >> 16) * (uint32_t)PW + jl];
+      }
+      acc &= v;
+    }
+    if ((s0 & 8) && !__any(acc != 0u)) break;  // every 16 literals: stop once nothing fires anywhere
+  }
+  const int pc = __popc(acc);
+  const int incl = group_scan_add<S>(pc);
+  const int R = lane_from(incl, gbase + S - 1);  // firing patches of the group's clause
+  // reservoir: the highest rank r <= R whose draw is below 1.0f / r
+  int best = 0;
+  bool open = R > 0;
+  int g0 = (R - 1) >> 2;  // draw site of the group's top ranks
+  while (__any(open)) {
+    const int gl = g0 - j;
+    int lb = 0;
+    if (open && gl >= 0) {
+      if (INJECT) {
+        for (int q = 0; q < 4; ++q) {
+          const int r = 4 * gl + 1 + q;
+          if (r <= R && inj[c * g.P + (r - 1)] < a.inv_rank[r]) lb = r;
+        }
+      } else {
+        const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = 4 * gl + 1 + q;
+          if (r <= R && uniform_from_word(word_of(z, q)) < a.inv_rank[r]) lb = r;
+        }
+      }
+    }
+    // lane j of a group holds ranks 4(g0 - j) + 1 .. + 4: the group's first lane with a hit
+    // holds the best
+    const uint32_t gh = (uint32_t)(__ballot(lb > 0) >> gbase) & gmask;
+    const int hit_best = lane_from(lb, gh ? gbase + __ffs((int)gh) - 1 : lane);
+    if (open) {
+      if (gh) {
+        best = hit_best;
+        open = false;
+      } else {
+        g0 -= S;
+        open = g0 >= 0;
+      }
+    }
+  }
+  // the patch of the best-th set bit of the group's firing bitmap
+  const int excl = incl - pc;
+  const bool here = best > 0 && j < PW && best > excl && best <= incl;
+  int p_here = 0;
+  if (here) {
+    uint32_t v = acc;
+    for (int q = 1; q < best - excl; ++q) v &= v - 1u;
+    p_here = j * 32 + __builtin_ctz(v);
+  }
+  const uint32_t hb = (uint32_t)(__ballot(here) >> gbase) & gmask;
+  const int p = lane_from(p_here, hb ? gbase + __ffs((int)hb) - 1 : lane);
+  return best > 0 ? p : -1;
+}
+
 // Phase A for one clause of a model with several patches, on the literal-major sample xt
 // ([L][PW] words, PW = ceil(P/32) <= 64; bit b of word j of literal l: literal l set in
 // patch 32j + b).  The clause fires on the patches where every included literal is set, so
@@ -918,6 +1026,63 @@ __device__ __forceinline__ void copy_to_lds(uint32_t* dst, const uint32_t* src, 
   }
 }
 
+// Phase A of the global kernel for several patches with literal lists: waves claim 64 / S
+// clauses at a time from *s_next and evaluate them in lane groups (eval_select_lm_group);
+// clauses without a list take the include-mask walk in global memory, a wave each.  Results
+// as the per-clause loop of train_global_body: selections, include counts, patch weights and
+// votes into s_part.
+template <bool INJECT, int S>
+__device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const float* inj, uint64_t t, int64_t c_begin,
+                                      int n_own, int* s_next, const uint16_t* s_lits, const int* s_nlit,
+                                      const uint32_t* xt, int* s_sel, int* s_ninc, const float* s_wg, long long* s_part) {
+  constexpr int NG = kWave / S;
+  const int lane = lane_id();
+  const int q = lane / S, jj = lane & (S - 1);
+  const int cap = g.list_cap;
+  for (;;) {
+    int idx0 = 0;
+    if (lane == 0) idx0 = atomicAdd(s_next, NG);
+    idx0 = lane_value(idx0, 0);
+    if (idx0 >= n_own) break;
+    const int idx = idx0 + q;
+    const bool in = idx < n_own;
+    const int ix = in ? idx : idx0;  // groups past the last clause read a valid one and discard it
+    const int nl = s_nlit[ix];
+    const bool listed = in && nl <= cap;
+    const int64_t c = c_begin + ix;
+    const int sel = eval_select_lm_group<INJECT, S>(a, g, inj, t, c, listed, s_lits + (int64_t)ix * cap, nl, xt,
+                                                    a.drop[c] == 1u);
+    if (listed) {
+      if (jj == 0) {
+        s_sel[idx] = sel;
+        s_ninc[idx] = nl;
+      }
+      if (sel >= 0) {
+        if (g.coalesced) {
+          for (int k = jj; k < g.K; k += S)
+            atomicAdd((unsigned long long*)&s_part[k], (unsigned long long)(long long)s_wg[(int64_t)ix * g.K + k]);
+        } else if (jj == 0) {
+          const int64_t k = c / g.per_bank;
+          atomicAdd((unsigned long long*)&s_part[k], (unsigned long long)(long long)s_wg[(int64_t)ix * g.K + k]);
+        }
+      }
+    }
+    for (unsigned long long r = __ballot(in && !listed && jj == 0); r; r &= r - 1ull) {
+      const int i2 = idx0 + (__ffsll((long long)r) - 1) / S;
+      const int64_t c2 = c_begin + i2;
+      int ninc;
+      const uint32_t* m = a.planes + (c2 * g.np + g.np - 1) * g.W;
+      const int sel2 = eval_select_lm<INJECT>(a, g, inj, c2, t, m, s_lits + (int64_t)i2 * cap, s_nlit[i2], cap, xt,
+                                              a.drop[c2] == 1u, &ninc);
+      if (lane == 0) {
+        s_sel[i2] = sel2;
+        s_ninc[i2] = ninc;
+      }
+      if (sel2 >= 0) add_partial(a, g, s_part, c2, s_wg + (int64_t)i2 * g.K);
+    }
+  }
+}
+
 // Clause state in global memory (L2/MALL resident across samples); any P.
 template <bool VANILLA, bool INJECT>
 __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom& g) {
@@ -989,7 +1154,15 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     __syncthreads();
 
     // ---- A: evaluation, reservoir selection, partial class sums
+    // Clauses with bitmaps of at most 16 words go four to a wave (eval_select_lm_group).  Two
+    // to a wave (32-lane groups) lost on config 4: claims of two clauses balance the waves
+    // worse (its phase A + barrier went from 10.8 to 11.5 us per sample).
+    const bool grouped = !VANILLA && literal_major(g) && cap > 0 && (g.P + 31) / 32 <= 16;
+    if (grouped)
+      global_eval_lm_groups<INJECT, 16>(a, g, inj, t, c_begin, n_own, &s_next, s_lits, s_nlit, xt, s_sel, s_ninc, s_wg,
+                                        s_part);
     for (;;) {
+      if (grouped) break;  // done above
       int idx = 0;
       if (lane == 0) idx = atomicAdd(&s_next, 1);
       idx = lane_value(idx, 0);
@@ -1005,18 +1178,21 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         s_sel[idx] = sel;
         s_ninc[idx] = ninc;
       }
-      if (sel >= 0) {
-        if (lane == 0) a.patch_w[c * g.P + sel] += 1;
-        add_partial(a, g, s_part, c, s_wg + (int64_t)idx * g.K);
-      }
+      if (sel >= 0) add_partial(a, g, s_part, c, s_wg + (int64_t)idx * g.K);
     }
     YTM_PROF_MARK(0);
     __syncthreads();
     YTM_PROF_MARK(1);
 
-    // ---- B + C
-    if (wave == 0)
+    // ---- B + C; wave 0 first adds the patch weights of the sample's selections (select_active,
+    // kernel.cu:305), deferred out of phase A so that no evaluation waits on these atomics
+    if (wave == 0) {
+      for (int idx = lane; idx < n_own; idx += kWave) {
+        const int sl = s_sel[idx];
+        if (sl >= 0) atomicAdd(&a.patch_w[(c_begin + idx) * g.P + sl], 1);
+      }
       exchange_class_sums(a, g, i, a.Y + (int64_t)i * g.K, a.bias, s_part, s_tgt, s_prob, &s_abort, &wait_ticks);
+    }
     YTM_PROF_MARK(2);
     if (threadIdx.x == 0) {
       s_next = 0;
@@ -1168,15 +1344,81 @@ __device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g,
   if (lane == 0) {
     sel_out[idx] = sel;
     ninc_out[idx] = ninc;
-    if (sel >= 0) {
-      if (g.P == 1)
-        s_pw[idx] += 1;
-      else
-        atomicAdd(&a.patch_w[c * g.P + sel], 1);
-    }
+    if (sel >= 0 && g.P == 1) s_pw[idx] += 1;  // several patches: added once final (train_resident_body)
   }
   if (sel >= 0 && (g.coalesced ? lane < g.K : lane == 0))
     atomicAdd((unsigned long long*)&part[kp], (unsigned long long)(long long)wk);
+}
+
+// Phase A of resident clauses with several patches on sample j, 64 / S clauses per wave pass
+// (eval_select_lm_group): passes b0, b0 + bstride, ... take clauses [b * 64/S, (b+1) * 64/S)
+// below n_own.  Results as resident_eval: selections, include counts, patch weights (global
+// memory) and the votes added into part.  Clauses without a literal list (more included
+// literals than its capacity) take resident_eval's include-mask walk, a wave each.  Needs
+// literal lists (list_cap > 0).
+template <bool INJECT, int S>
+__device__ void resident_eval_lm_groups(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int b0, int bstride,
+                                        int n_own, const uint32_t* s_planes, const float* s_w, const int* s_drop,
+                                        const uint32_t* s_x, const uint32_t* s_xt, const float* s_usel,
+                                        const uint16_t* s_lits, const int* s_nlit, int* sel_out, int* ninc_out,
+                                        int* s_pw, long long* part) {
+  constexpr int NG = kWave / S;
+  const int lane = lane_id();
+  const int q = lane / S, jj = lane & (S - 1);
+  const uint64_t t = a.step0 + (uint64_t)j;
+  const float* inj = INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr;
+  const int cap = g.list_cap;
+  const uint32_t* xt = s_xt + (int64_t)(j & 1) * g.L * ((g.P + 31) / 32);
+  for (int b = b0; b * NG < n_own; b += bstride) {
+    const int idx = b * NG + q;
+    const bool in = idx < n_own;
+    const int ix = in ? idx : b * NG;  // groups past the last clause read a valid one and discard it
+    const int nl = s_nlit[ix];
+    const bool listed = in && nl <= cap;
+    const int64_t c = c_begin + ix;
+    const int sel = eval_select_lm_group<INJECT, S>(a, g, inj, t, c, listed, s_lits + (int64_t)ix * cap, nl, xt,
+                                                    s_drop[ix] != 0);
+    if (listed) {
+      if (jj == 0) {
+        sel_out[idx] = sel;
+        ninc_out[idx] = nl;
+      }
+      if (sel >= 0) {
+        if (g.coalesced) {
+          for (int k = jj; k < g.K; k += S)
+            atomicAdd((unsigned long long*)&part[k], (unsigned long long)(long long)s_w[(int64_t)ix * g.K + k]);
+        } else if (jj == 0) {
+          const int64_t k = c / g.per_bank;
+          atomicAdd((unsigned long long*)&part[k], (unsigned long long)(long long)s_w[(int64_t)ix * g.K + k]);
+        }
+      }
+    }
+    // clauses without a literal list, a wave each
+    for (unsigned long long r = __ballot(in && !listed && jj == 0); r; r &= r - 1ull)
+      resident_eval<INJECT>(a, g, j, c_begin, b * NG + (__ffsll((long long)r) - 1) / S, s_planes, s_w, s_drop, s_x,
+                            s_xt, s_usel, s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
+  }
+}
+
+// Phase A of the resident clauses idx0, idx0 + stride, ... with several patches on sample j:
+// in lane groups when the literal lists and the patch bitmap allow, else a wave per clause.
+template <bool INJECT>
+__device__ __forceinline__ void resident_eval_lm(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int idx0,
+                                                 int stride, int n_own, const uint32_t* s_planes, const float* s_w,
+                                                 const int* s_drop, const uint32_t* s_x, const uint32_t* s_xt,
+                                                 const float* s_usel, const uint16_t* s_lits, const int* s_nlit,
+                                                 int* sel_out, int* ninc_out, int* s_pw, long long* part) {
+  const int64_t PW = (g.P + 31) / 32;
+  if (g.list_cap > 0 && PW <= 16)
+    resident_eval_lm_groups<INJECT, 16>(a, g, j, c_begin, idx0, stride, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel,
+                                        s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
+  else if (g.list_cap > 0 && PW <= 32)
+    resident_eval_lm_groups<INJECT, 32>(a, g, j, c_begin, idx0, stride, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel,
+                                        s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
+  else
+    for (int idx = idx0; idx < n_own; idx += stride)
+      resident_eval<INJECT>(a, g, j, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, sel_out,
+                            ninc_out, s_pw, part);
 }
 
 // Phase A of the one-patch clauses idx0, idx0 + stride, ... (below n_own) on sample j, by
@@ -1250,6 +1492,19 @@ __device__ void resident_eval_multi(const TrainArgs& a, const Geom& g, int j, in
   }
 }
 
+// Patch weights of a sample's final selections with several patches (select_active,
+// kernel.cu:305), added by wave 0 while it waits for the sample's class sums: the atomics'
+// round trips then hold up no evaluation (a later load's wait would include them).  One
+// patch keeps its patch weights in LDS instead.
+__device__ __forceinline__ void flush_patch_weights(const TrainArgs& a, const Geom& g, int64_t c_begin, int n_own,
+                                                    const int* sel) {
+  if (g.P == 1) return;
+  for (int idx = lane_id(); idx < n_own; idx += kWave) {
+    const int sl = sel[idx];
+    if (sl >= 0) atomicAdd(&a.patch_w[(c_begin + idx) * g.P + sl], 1);
+  }
+}
+
 // Fused D1 (train_resident_body): the decisions of sample i were taken while other waves
 // could still be reading the clause's weights for sample i+1, so the task's wave, before its
 // literal updates, takes back the clause's speculative votes of sample i+1 (weights from
@@ -1268,12 +1523,7 @@ __device__ __forceinline__ void commit_fused_task(const TrainArgs& a, const Geom
     if (spec_sel >= 0) atomicAdd((unsigned long long*)&part_next[k], (unsigned long long)(-(long long)*wp));
     *wp = task_w[k];
   }
-  if (lane == 0 && spec_sel >= 0) {
-    if (g.P == 1)
-      s_pw[idx] -= 1;
-    else
-      atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
-  }
+  if (lane == 0 && spec_sel >= 0 && g.P == 1) s_pw[idx] -= 1;
 }
 
 // Training with each workgroup's clause state resident in LDS for the whole launch:
@@ -1386,9 +1636,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       resident_eval_multi<INJECT>(a, g, 0, c_begin, wave, nwv, n_own, s_planes, s_w, s_drop, s_x, s_usel, s_sel, s_ninc,
                                   s_pw, s_part[0]);
     else
-      for (int idx = wave; idx < n_own; idx += nwv)
-        resident_eval<INJECT>(a, g, 0, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, s_sel, s_ninc,
-                              s_pw, s_part[0]);
+      resident_eval_lm<INJECT>(a, g, 0, c_begin, wave, nwv, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit,
+                               s_sel, s_ninc, s_pw, s_part[0]);
   }
   __syncthreads();
   prof_last = __builtin_amdgcn_s_memrealtime();
@@ -1426,6 +1675,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       }
       if (fused) {
         exchange_publish(a, g, i, s_part[b2]);
+        flush_patch_weights(a, g, c_begin, n_own, s_sel + b2 * cpw);
         // the decisions' inputs, loaded while the class sums are exchanged; lane (jc, kk)
         // takes class kk of clause p * cpp + jc in pass p
         const ClassPrep cp = class_prep(g, s_y[b3 * g.K + kk]);
@@ -1488,7 +1738,12 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         }
         YTM_PROF_MARK(2);
       } else {
-        exchange_class_sums(a, g, i, s_y + b3 * g.K, s_bias, s_part[b2], s_tgt, s_prob, &s_abort, &wait_ticks);
+        exchange_publish(a, g, i, s_part[b2]);
+        flush_patch_weights(a, g, c_begin, n_own, s_sel + b2 * cpw);
+        long long S = 0;
+        if (exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part[b2], &S, &s_abort, &wait_ticks) &&
+            lane < g.K)
+          class_targets(g, lane, S + (long long)s_bias[lane], s_y + b3 * g.K, s_tgt, s_prob);
         YTM_PROF_MARK(0);
       }
     } else {
@@ -1515,9 +1770,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
           resident_eval_multi<INJECT>(a, g, i + 1, c_begin, wave - 1, nwv - 1, n_own, s_planes, s_w, s_drop, s_x, s_usel,
                                       s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
         else
-          for (int idx = wave - 1; idx < n_own; idx += nwv - 1)
-            resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit,
-                                  s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+          resident_eval_lm<INJECT>(a, g, i + 1, c_begin, wave - 1, nwv - 1, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel,
+                                   s_lits, s_nlit, s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
       }
       if (a.profile == 2) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
       if (i + 2 < a.N) {
@@ -1554,12 +1808,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
           if (spec_sel >= 0) {
             if (g.coalesced ? lane < g.K : lane == 0)
               atomicAdd((unsigned long long*)&s_part[b2n][kp], (unsigned long long)(-(long long)wold));
-            if (lane == 0) {
-              if (g.P == 1)
-                s_pw[idx] -= 1;
-              else
-                atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
-            }
+            if (lane == 0 && g.P == 1) s_pw[idx] -= 1;
           }
           if (lane == 0) {
             ++my_updates;
@@ -1608,12 +1857,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
           const bool leader = changes && kk == 0;
           my_updates += (unsigned long long)__popcll(__ballot(leader));
           if (leader) {
-            if (spec_sel >= 0) {
-              if (g.P == 1)
-                s_pw[ix] -= 1;
-              else
-                atomicAdd(&a.patch_w[c * g.P + spec_sel], -1);
-            }
+            if (spec_sel >= 0 && g.P == 1) s_pw[ix] -= 1;
             const unsigned long long rng = INJECT ? 0ull : (m1a | m1b);
             const int tk = atomicAdd(&s_ntask[b2], 1);
             const int sb = INJECT ? 0 : atomicAdd(&s_nslot[b2], __popcll(rng));
