@@ -23,7 +23,11 @@ enum {
     YTM_OK = 0,
     YTM_EINVAL = 1,   /* bad argument / unsupported configuration */
     YTM_EHIP = 2,     /* HIP runtime error */
-    YTM_ETIMEOUT = 3, /* a persistent kernel's bounded wait expired */
+    YTM_ETIMEOUT = 3, /* a persistent kernel's bounded wait expired (2 s of real time, which
+                         also runs while the GPU is preempted); the model's state is then a mix
+                         of samples, and ytm_fit*, ytm_score* and ytm_transform refuse it
+                         (YTM_EINVAL) until ytm_set_ta_state, ytm_set_weights and
+                         ytm_set_patch_weights have all loaded a state again */
     YTM_ERANGE = 4    /* state value outside what the model can represent */
 };
 

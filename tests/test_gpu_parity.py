@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 
 ytm_amd = pytest.importorskip("ytm_amd")
 from ytm_amd import MultiClassTM, MultiOutputTM  # noqa: E402
+from ytm_amd._lib import YtmError  # noqa: E402
 
 orc.set_threads(min(16, os.cpu_count() or 1))
 
@@ -298,6 +299,34 @@ def test_launch_shape_independence(monkeypatch):
     for s in states[1:]:
         for a, b in zip(states[0], s):
             np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("cfg,clauses", [(2, 100), (3, 30)])  # streaming kernel; resident conv kernel
+def test_timeout_leaves_model_refusing_until_reloaded(monkeypatch, cfg, clauses):
+    """A class-sum wait that expires (forced from the host: YTM_TRAIN_TEST_TIMEOUT makes every
+    wait miss its sums and expire at once, and every workgroup exits normally) returns
+    YTM_ETIMEOUT; the model then refuses fit and score until a whole state is loaded again,
+    and trains on from there like the oracle does."""
+    tm, ref, X, y, Xt, yt = pair(cfg, 60, 20, clauses=clauses)
+    encX = tm.encode(X)
+    tm.fit(encX, y, is_X_encoded=True)
+    ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+    state = tm.get_state_dict()
+    monkeypatch.setenv("YTM_TRAIN_TEST_TIMEOUT", "1")
+    with pytest.raises(YtmError, match="bounded wait"):
+        tm.fit(encX, y, is_X_encoded=True)
+    monkeypatch.delenv("YTM_TRAIN_TEST_TIMEOUT")
+    with pytest.raises(ValueError, match="timed out"):
+        tm.fit(encX, y, is_X_encoded=True)
+    with pytest.raises(ValueError, match="timed out"):
+        tm.score(tm.encode(Xt), is_X_encoded=True)
+    tm.load_state_dict({"state": state})
+    # the failed launch advanced neither the model's step nor the oracle's: both go on alike
+    assert tm.stats()["step"] == ref.step
+    tm.fit(encX, y, is_X_encoded=True)
+    assert tm.stats()["last_fit_updates"] == ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+    assert_state_equal(tm, ref, "after reloading")
+    np.testing.assert_array_equal(tm.score(tm.encode(Xt), is_X_encoded=True), ref.score(ref.encode(Xt)))
 
 
 # ------------------------------------------------------------------ inference

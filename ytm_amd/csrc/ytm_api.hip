@@ -41,6 +41,12 @@ struct ytm_model {
   // Upper bound of |clause weight|: 1 after initialisation, the largest loaded magnitude
   // after ytm_set_weights, and + 1 per trained sample (a sample moves a weight by at most 1).
   double w_bound = 1.0;
+  // A training launch whose bounded wait expired stops each workgroup at its own sample, so
+  // the state is then a mix of samples: the model refuses fit, score and transform until a
+  // whole state is loaded again (the bits of the setters called since: 1 TA states, 2
+  // weights, 4 patch weights).
+  bool invalid = false;
+  int reloaded = 0;
   ytm_stats stats;
 };
 
@@ -155,6 +161,24 @@ int ensure_slots(ytm_model* m, size_t bytes) {
   HIP_TRY(hipMalloc(&m->d_slots, bytes));
   m->slots_bytes = bytes;
   return YTM_OK;
+}
+
+int check_valid(const ytm_model* m) {
+  if (m->invalid)
+    return fail(YTM_EINVAL, "the model's state is a mix of samples after a training launch timed out; load a whole "
+                            "state (TA states, weights and patch weights) or create the model again");
+  return YTM_OK;
+}
+
+// A setter of part of the state succeeded: once all three parts are loaded again the model
+// is usable.
+void note_reload(ytm_model* m, int part) {
+  if (!m->invalid) return;
+  m->reloaded |= part;
+  if (m->reloaded == 7) {
+    m->invalid = false;
+    m->reloaded = 0;
+  }
 }
 
 int upload(void** dst, const void* src, size_t bytes, hipStream_t s) {
@@ -476,6 +500,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   if (!m || !ds || ds->m != m) return fail(YTM_EINVAL, "dataset does not belong to this model");
   if (!ds->d_Y) return fail(YTM_EINVAL, "dataset has no targets");
   if (first < 0 || count < 0 || first + count > ds->N) return fail(YTM_EINVAL, "sample range out of bounds");
+  if (int rc = check_valid(m)) return rc;
   m->stats.last_fit_samples = 0;
   m->stats.last_fit_updates = 0;
   m->stats.last_fit_kernel_ms = 0.0;
@@ -595,6 +620,8 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.rng_slots = rng_slots;
     const char* prof_env = std::getenv("YTM_TRAIN_PROFILE");
     a.profile = prof_env ? std::max(0, std::atoi(prof_env)) : 0;
+    const char* tt_env = std::getenv("YTM_TRAIN_TEST_TIMEOUT");  // test hook of the timeout path
+    a.test_timeout = tt_env && std::atoi(tt_env) > 0;
     a.g = g;
     FIT_TRY(hipEventRecord(m->ev0, m->stream));
     if (jit_fn)
@@ -609,11 +636,14 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     ++launches;
     int herr[4] = {0, 0, 0, 0};
     FIT_TRY(hipMemcpy(herr, m->d_err, sizeof(herr), hipMemcpyDeviceToHost));
-    if (herr[0])
+    if (herr[0]) {
+      m->invalid = true;
+      m->reloaded = 0;
       return finish(fail(YTM_ETIMEOUT, "training kernel: the bounded wait for the class sums of sample " +
                                            std::to_string(s + herr[1]) + " expired in workgroup " +
                                            std::to_string(herr[2]) + " (count seen " + std::to_string(herr[3]) +
                                            ", grid " + std::to_string(grid) + ", groups " + std::to_string(D) + ")"));
+    }
   }
   unsigned long long cnt[16] = {0};
   FIT_TRY(hipMemcpy(cnt, m->d_counters, sizeof(cnt), hipMemcpyDeviceToHost));
@@ -726,6 +756,7 @@ extern "C" {
 
 int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (!m || !ds || ds->m != m || (ds->N > 0 && !class_sums)) return fail(YTM_EINVAL, "bad score arguments");
+  if (int rc = check_valid(m)) return rc;
   const Geom& g = m->g;
   const int64_t N = ds->N;
   if (N == 0) return YTM_OK;
@@ -752,6 +783,7 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
 
 int ytm_score_dataset_noalloc(ytm_model* m, const ytm_dataset* ds, float* d_class_sums) {
   if (!m || !ds || ds->m != m || (ds->N > 0 && !d_class_sums)) return fail(YTM_EINVAL, "bad score arguments");
+  if (int rc = check_valid(m)) return rc;
   const Geom& g = m->g;
   const int64_t N = ds->N;
   if (N == 0) return YTM_OK;
@@ -800,6 +832,7 @@ int ytm_score(ytm_model* m, const uint32_t* encX, int64_t N, float* class_sums) 
 int ytm_transform(ytm_model* m, const uint32_t* encX, int64_t N, int mode, uint32_t* out) {
   if (!m || N < 0 || mode < 0 || mode > 2 || (N > 0 && (!encX || !out)))
     return fail(YTM_EINVAL, "bad transform arguments");
+  if (int rc = check_valid(m)) return rc;
   if (N == 0) return YTM_OK;
   const Geom& g = m->g;
   const int64_t PW = (g.P + 31) / 32;
@@ -873,6 +906,7 @@ int ytm_set_ta_state(ytm_model* m, const uint32_t* in) {
   if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
   (void)hipFree(d);
   if (e != hipSuccess) return fail(YTM_EHIP, std::string("set_ta_state failed: ") + hipGetErrorString(e));
+  note_reload(m, 1);
   return YTM_OK;
 }
 
@@ -895,6 +929,7 @@ int ytm_set_weights(ytm_model* m, const float* in) {
   double bound = 0.0;
   for (int64_t i = 0; i < m->g.C * m->g.K; ++i) bound = std::max(bound, (double)std::fabs(in[i]));
   m->w_bound = bound;
+  note_reload(m, 2);
   return YTM_OK;
 }
 
@@ -909,6 +944,7 @@ int ytm_set_patch_weights(ytm_model* m, const int32_t* in) {
   if (!m || !in) return fail(YTM_EINVAL, "null argument");
   HIP_TRY(hipMemcpyAsync(m->d_pw, in, (size_t)(m->g.C * m->g.P) * 4, hipMemcpyHostToDevice, m->stream));
   HIP_TRY(hipStreamSynchronize(m->stream));
+  note_reload(m, 4);
   return YTM_OK;
 }
 

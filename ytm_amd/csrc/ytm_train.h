@@ -923,17 +923,19 @@ __device__ __forceinline__ bool exchange_wait(const TrainArgs& a, const Geom& g,
   }
   const ExchangeRow r = exchange_row(a, g, i);
   const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+  // a count no word reaches under the test hook: every wait then expires
+  const unsigned long long complete = r.poll_count + (a.test_timeout ? 1ull : 0ull);
   unsigned long long v = 0;
   for (unsigned polls = 1;; ++polls) {
     bool ok = true;
     if (want) {
       v = __hip_atomic_load(&r.poll[kq], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok = ((v + (1ull << 43)) >> 44) == r.poll_count;
+      ok = ((v + (1ull << 43)) >> 44) == complete;
     }
     if (__all(ok)) break;
     // the clock is read every 16th poll: each read is a scalar-memory round trip that would
     // otherwise lengthen every poll (the bound stays in real time)
-    if ((polls & 15u) == 0u && __builtin_amdgcn_s_memrealtime() - t_start > kWaitTicks) {
+    if ((polls & 15u) == 0u && __builtin_amdgcn_s_memrealtime() - t_start > (a.test_timeout ? 0 : kWaitTicks)) {
       // Record the first stall: err = {1, sample, workgroup, count seen by lane 0}.
       if (lane == 0) {
         *s_abort = 1;
@@ -2095,6 +2097,8 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       const long long bias_k = (long long)a.bias[k];
       int j = gen_start;
       int stop = -1;
+      // a count no word reaches under the test hook: every wait then expires
+      const unsigned long long complete = (unsigned long long)G + (a.test_timeout ? 1ull : 0ull);
       while (j < a.N) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         bool here = q < nq && j + q < a.N;  // this lane's (row, class) exists
@@ -2105,7 +2109,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           if (here) {
             v = __hip_atomic_load(&a.slots[(row_base + (j + q - gen_start)) * ks + k], __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT);
-            ok = ((v + (1ull << 43)) >> 44) == (unsigned long long)G;
+            ok = ((v + (1ull << 43)) >> 44) == complete;
           }
           // complete rows from j on: the first row with an incomplete word ends them
           const unsigned long long bad = __ballot(here && !ok);
@@ -2114,7 +2118,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           ncomp = first_bad < avail ? first_bad : avail;
           if (ncomp > 0) break;
           if ((polls & 15u) == 0u && lds_load(&ctl.abort)) break;  // an evaluation wave gave up
-          if ((polls & 15u) == 0u && __builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) {
+          if ((polls & 15u) == 0u && __builtin_amdgcn_s_memrealtime() - t0 > (a.test_timeout ? 0 : kWaitTicks)) {
             if (lane == 0) {
               lds_store(&ctl.abort, 1);
               if (atomicCAS(a.err, 0, 1) == 0) {

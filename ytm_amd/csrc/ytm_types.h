@@ -102,6 +102,7 @@ struct TrainArgs {
   int cpw;                   // max clauses owned by one workgroup
   int rng_slots;             // literal-draw slots precomputed per sample (resident kernel)
   int profile;               // accumulate per-phase times into counters[4..11]
+  int test_timeout;          // test hook: class-sum waits never see their sums and expire at once
   Geom g;
 };
 
