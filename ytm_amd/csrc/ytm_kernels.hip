@@ -1015,11 +1015,13 @@ size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g) {
   // weights [cpw]; targets [3][K]; bias [K]; rank-1 draws [3][cpw]; Q-skip and update
   // draws [3][cpw][K] each; task clause / first slot [cpw]; staged task weights [cpw][K];
   // slot clause / class [R]; slot plane groups [R][W][kPreGroups][4].
-  // Several patches add the literal-major samples [2][L][PW] after the task masks.
+  // Several patches add the literal-major samples [2][L][PW] after the task masks and the
+  // reservoir thresholds [P+1] at the end.
   const size_t C = (size_t)cpw, K = (size_t)g.K, W = (size_t)g.W, R = (size_t)rng_slots;
   const size_t xt = g.P > 1 ? (size_t)(2 * g.L * ((g.P + 31) / 32)) * 4 : 0;
   return 3 * C * 8 + lists + xt + C * (size_t)g.np * W * 4 + C * K * 4 + 3 * W * 4 + 4 * C * 4 + 2 * C * 4 + 3 * K * 4 +
-         K * 4 + 3 * C * 4 + 6 * C * K * 4 + 2 * C * 4 + C * K * 4 + 2 * R * 4 + R * W * kPreGroups * 4 * 4;
+         K * 4 + 3 * C * 4 + 6 * C * K * 4 + 2 * C * 4 + C * K * 4 + 2 * R * 4 + R * W * kPreGroups * 4 * 4 +
+         (g.P > 1 ? (size_t)(g.P + 1) * 4 : 0);  // reservoir thresholds [P+1]
 }
 
 size_t stream_lds_bytes(const Geom& g, int threads) {

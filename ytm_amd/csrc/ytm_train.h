@@ -101,7 +101,7 @@ __device__ __forceinline__ uint32_t literal_draw_mask(const TrainArgs& a, const 
 // a time.  Wave-uniform.
 template <bool INJECT>
 __device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t,
-                                              int R) {
+                                              int R, const float* inv_rank) {
   const int lane = lane_id();
   int best = 0;
   for (int g0 = (R - 1) >> 2; g0 >= 0; g0 -= kWave) {
@@ -111,14 +111,14 @@ __device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g,
       if (INJECT) {
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * gl + 1 + j;
-          if (r <= R && inj[c * g.P + (r - 1)] < a.inv_rank[r]) lb = r;
+          if (r <= R && inj[c * g.P + (r - 1)] < inv_rank[r]) lb = r;
         }
       } else {
         const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * gl + 1 + j;
-          if (r <= R && uniform_from_word(word_of(z, j)) < a.inv_rank[r]) lb = r;
+          if (r <= R && uniform_from_word(word_of(z, j)) < inv_rank[r]) lb = r;
         }
       }
     }
@@ -137,14 +137,14 @@ __device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g,
 // Returns -1 when none is selected.  Wave-uniform.
 template <bool INJECT>
 __device__ __forceinline__ int select_from_bitmap(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t,
-                                                  uint32_t acc) {
+                                                  uint32_t acc, const float* inv_rank) {
   const int lane = lane_id();
   const int PW = (int)((g.P + 31) / 32);
   const int pc = lane < PW ? __popc(acc) : 0;
   const int incl = wave_inclusive_scan(pc);
   const int R = lane_value(incl, kWave - 1);
   if (R == 0) return -1;
-  const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R);
+  const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R, inv_rank);
   if (best == 0) return -1;
   const int excl = incl - pc;
   const bool here = lane < PW && best > excl && best <= incl;
@@ -351,7 +351,8 @@ __device__ __forceinline__ int lane_from(int v, int src) { return __builtin_amdg
 // same in every lane of the group.
 template <bool INJECT, int S>
 __device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const float* inj, uint64_t t, int64_t c,
-                                    bool valid, const uint16_t* list, int n, const uint32_t* xt, bool dropped) {
+                                    bool valid, const uint16_t* list, int n, const uint32_t* xt, bool dropped,
+                                    const float* inv_rank) {
   const int lane = lane_id();
   const int j = lane & (S - 1);
   const int gbase = lane - j;
@@ -391,14 +392,14 @@ __device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const flo
       if (INJECT) {
         for (int q = 0; q < 4; ++q) {
           const int r = 4 * gl + 1 + q;
-          if (r <= R && inj[c * g.P + (r - 1)] < a.inv_rank[r]) lb = r;
+          if (r <= R && inj[c * g.P + (r - 1)] < inv_rank[r]) lb = r;
         }
       } else {
         const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = 4 * gl + 1 + q;
-          if (r <= R && uniform_from_word(word_of(z, q)) < a.inv_rank[r]) lb = r;
+          if (r <= R && uniform_from_word(word_of(z, q)) < inv_rank[r]) lb = r;
         }
       }
     }
@@ -441,7 +442,7 @@ __device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const flo
 template <bool INJECT>
 __device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, const uint32_t* m,
                               const uint16_t* list, int nlist, int cap, const uint32_t* xt, bool dropped,
-                              int* ninc_out) {
+                              int* ninc_out, const float* inv_rank) {
   const int lane = lane_id();
   int ninc;
   if (cap > 0 && nlist <= cap) {
@@ -462,7 +463,7 @@ __device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* in
   uint32_t acc = all_patches_word(g);
   if (ninc != 0)
     acc = (cap > 0 && nlist <= cap) ? firing_from_list(g, list, nlist, xt, acc) : firing_from_mask(g, m, xt, acc);
-  return select_from_bitmap<INJECT>(a, g, inj, c, t, acc);
+  return select_from_bitmap<INJECT>(a, g, inj, c, t, acc, inv_rank);
 }
 
 // Phase A for one clause (wave-uniform): returns the selected patch or -1 and the
@@ -528,7 +529,7 @@ __device__ int eval_select(const TrainArgs& a, const Geom& g, const float* inj, 
       R += __popcll(b);
     }
     if (R == 0) return -1;
-    const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R);
+    const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R, a.inv_rank);
     if (best == 0) return -1;
     // Patch of the best-th set bit of the firing bitmap.
     const int pc = lane < nch ? __popcll(myfire) : 0;
@@ -1036,7 +1037,8 @@ __device__ __forceinline__ void copy_to_lds(uint32_t* dst, const uint32_t* src, 
 template <bool INJECT, int S>
 __device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const float* inj, uint64_t t, int64_t c_begin,
                                       int n_own, int* s_next, const uint16_t* s_lits, const int* s_nlit,
-                                      const uint32_t* xt, int* s_sel, int* s_ninc, const float* s_wg, long long* s_part) {
+                                      const uint32_t* xt, int* s_sel, int* s_ninc, const float* s_wg, long long* s_part,
+                                      const float* inv_rank) {
   constexpr int NG = kWave / S;
   const int lane = lane_id();
   const int q = lane / S, jj = lane & (S - 1);
@@ -1053,7 +1055,7 @@ __device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const f
     const bool listed = in && nl <= cap;
     const int64_t c = c_begin + ix;
     const int sel = eval_select_lm_group<INJECT, S>(a, g, inj, t, c, listed, s_lits + (int64_t)ix * cap, nl, xt,
-                                                    a.drop[c] == 1u);
+                                                    a.drop[c] == 1u, inv_rank);
     if (listed) {
       if (jj == 0) {
         s_sel[idx] = sel;
@@ -1075,7 +1077,7 @@ __device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const f
       int ninc;
       const uint32_t* m = a.planes + (c2 * g.np + g.np - 1) * g.W;
       const int sel2 = eval_select_lm<INJECT>(a, g, inj, c2, t, m, s_lits + (int64_t)i2 * cap, s_nlit[i2], cap, xt,
-                                              a.drop[c2] == 1u, &ninc);
+                                              a.drop[c2] == 1u, &ninc, inv_rank);
       if (lane == 0) {
         s_sel[i2] = sel2;
         s_ninc[i2] = ninc;
@@ -1162,7 +1164,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     const bool grouped = !VANILLA && literal_major(g) && cap > 0 && (g.P + 31) / 32 <= 16;
     if (grouped)
       global_eval_lm_groups<INJECT, 16>(a, g, inj, t, c_begin, n_own, &s_next, s_lits, s_nlit, xt, s_sel, s_ninc, s_wg,
-                                        s_part);
+                                        s_part, a.inv_rank);
     for (;;) {
       if (grouped) break;  // done above
       int idx = 0;
@@ -1174,7 +1176,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : a.planes + (c * g.np + g.np - 1) * g.W;
       const int sel = (!VANILLA && literal_major(g))
                           ? eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * cap,
-                                                   cap > 0 ? s_nlit[idx] : 0, cap, xt, a.drop[c] == 1u, &ninc)
+                                                   cap > 0 ? s_nlit[idx] : 0, cap, xt, a.drop[c] == 1u, &ninc, a.inv_rank)
                           : eval_select<VANILLA, INJECT>(a, g, inj, c, t, m, xe, a.drop[c] == 1u, -1.0f, &ninc);
       if (lane == 0) {
         s_sel[idx] = sel;
@@ -1285,14 +1287,14 @@ __device__ __forceinline__ void stage_sample(const TrainArgs& a, const Geom& g, 
 }
 
 // Counter-stream draws of sample i for the workgroup's clauses, computed ahead of use
-// into buffer buf: the reservoir draw of rank 1 (s_usel[buf][idx]) and the Q-skip / update
+// into buffer buf: the reservoir draw of rank 1 (s_usel[buf][idx], one patch only) and the Q-skip / update
 // draws (s_uq / s_uu [buf][idx][k]).  Threads [first, first + count) take part.
 __device__ __forceinline__ void precompute_draws(const TrainArgs& a, const Geom& g, int i, int buf, int64_t c_begin,
                                                  int n_own, float* s_usel, float* s_uq, float* s_uu, int first,
                                                  int count) {
   const uint64_t t = a.step0 + (uint64_t)i;
   const int kn = g.coalesced ? (int)g.K : 1;
-  const int per = kn + 1;
+  const int per = kn + (g.P == 1 ? 1 : 0);  // the rank-1 draw serves one-patch models only
   for (int j = first; j < n_own * per; j += count) {
     const int idx = j / per, r = j % per;
     const int64_t c = c_begin + idx;
@@ -1315,6 +1317,42 @@ __device__ __forceinline__ void stage_xt(const TrainArgs& a, const Geom& g, int 
   copy_to_lds(s_xt + (int64_t)buf * n, a.XT + (int64_t)i * n, n, first, count);
 }
 
+// Staging of a literal-major sample around phase A: xt_prefetch issues the global loads of
+// the first kXtPre word pairs per thread into registers, which nothing waits on until
+// xt_commit stores them into LDS buffer buf and copies the rest (phase A in between reads
+// only LDS).  Threads [first, first + count) take part.  An odd word count is copied whole
+// by xt_commit.
+constexpr int kXtPre = 2;
+struct XtPre {
+  uint2 v[kXtPre];
+};
+__device__ __forceinline__ void xt_prefetch(const TrainArgs& a, const Geom& g, int i, int first, int count, XtPre* r) {
+  const int64_t n = g.L * ((g.P + 31) / 32);
+  if (n & 1) return;
+  const uint2* src = (const uint2*)(a.XT + (int64_t)i * n);
+#pragma unroll
+  for (int b = 0; b < kXtPre; ++b) {
+    const int64_t j = first + (int64_t)b * count;
+    if (j < n / 2) r->v[b] = src[j];
+  }
+}
+__device__ __forceinline__ void xt_commit(const TrainArgs& a, const Geom& g, int i, int buf, uint32_t* s_xt, int first,
+                                          int count, const XtPre& r) {
+  const int64_t n = g.L * ((g.P + 31) / 32);
+  if (n & 1) {
+    stage_xt(a, g, i, buf, s_xt, first, count);
+    return;
+  }
+  const uint2* src = (const uint2*)(a.XT + (int64_t)i * n);
+  uint2* dst = (uint2*)(s_xt + (int64_t)buf * n);
+#pragma unroll
+  for (int b = 0; b < kXtPre; ++b) {
+    const int64_t j = first + (int64_t)b * count;
+    if (j < n / 2) dst[j] = r.v[b];
+  }
+  for (int64_t j = first + (int64_t)kXtPre * count; j < n / 2; j += count) dst[j] = src[j];
+}
+
 // Phase A of one resident clause (local index idx) on sample j, by one wave: selection
 // (sel[idx]), include count (ninc[idx]), patch weight and the clause's votes added into
 // part.  One patch: the sample's words are s_x[j % 3], the rank-1 draw s_usel[j % 3] and
@@ -1324,8 +1362,8 @@ template <bool INJECT>
 __device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int idx,
                                               const uint32_t* s_planes, const float* s_w, const int* s_drop,
                                               const uint32_t* s_x, const uint32_t* s_xt, const float* s_usel,
-                                              const uint16_t* s_lits, const int* s_nlit, int* sel_out, int* ninc_out,
-                                              int* s_pw, long long* part) {
+                                              const float* inv_rank, const uint16_t* s_lits, const int* s_nlit,
+                                              int* sel_out, int* ninc_out, int* s_pw, long long* part) {
   const int lane = lane_id();
   const int64_t c = c_begin + idx;
   const uint64_t t = a.step0 + (uint64_t)j;
@@ -1342,7 +1380,8 @@ __device__ __forceinline__ void resident_eval(const TrainArgs& a, const Geom& g,
                                              INJECT ? -1.0f : s_usel[(j % 3) * a.cpw + idx], &ninc);
   else
     sel = eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * g.list_cap, g.list_cap > 0 ? s_nlit[idx] : 0,
-                                 g.list_cap, s_xt + (int64_t)(j & 1) * g.L * ((g.P + 31) / 32), dropped, &ninc);
+                                 g.list_cap, s_xt + (int64_t)(j & 1) * g.L * ((g.P + 31) / 32), dropped, &ninc,
+                                 inv_rank);
   if (lane == 0) {
     sel_out[idx] = sel;
     ninc_out[idx] = ninc;
@@ -1362,8 +1401,8 @@ template <bool INJECT, int S>
 __device__ void resident_eval_lm_groups(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int b0, int bstride,
                                         int n_own, const uint32_t* s_planes, const float* s_w, const int* s_drop,
                                         const uint32_t* s_x, const uint32_t* s_xt, const float* s_usel,
-                                        const uint16_t* s_lits, const int* s_nlit, int* sel_out, int* ninc_out,
-                                        int* s_pw, long long* part) {
+                                        const float* inv_rank, const uint16_t* s_lits, const int* s_nlit,
+                                        int* sel_out, int* ninc_out, int* s_pw, long long* part) {
   constexpr int NG = kWave / S;
   const int lane = lane_id();
   const int q = lane / S, jj = lane & (S - 1);
@@ -1379,7 +1418,7 @@ __device__ void resident_eval_lm_groups(const TrainArgs& a, const Geom& g, int j
     const bool listed = in && nl <= cap;
     const int64_t c = c_begin + ix;
     const int sel = eval_select_lm_group<INJECT, S>(a, g, inj, t, c, listed, s_lits + (int64_t)ix * cap, nl, xt,
-                                                    s_drop[ix] != 0);
+                                                    s_drop[ix] != 0, inv_rank);
     if (listed) {
       if (jj == 0) {
         sel_out[idx] = sel;
@@ -1398,7 +1437,7 @@ __device__ void resident_eval_lm_groups(const TrainArgs& a, const Geom& g, int j
     // clauses without a literal list, a wave each
     for (unsigned long long r = __ballot(in && !listed && jj == 0); r; r &= r - 1ull)
       resident_eval<INJECT>(a, g, j, c_begin, b * NG + (__ffsll((long long)r) - 1) / S, s_planes, s_w, s_drop, s_x,
-                            s_xt, s_usel, s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
+                            s_xt, s_usel, inv_rank, s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
   }
 }
 
@@ -1408,19 +1447,20 @@ template <bool INJECT>
 __device__ __forceinline__ void resident_eval_lm(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int idx0,
                                                  int stride, int n_own, const uint32_t* s_planes, const float* s_w,
                                                  const int* s_drop, const uint32_t* s_x, const uint32_t* s_xt,
-                                                 const float* s_usel, const uint16_t* s_lits, const int* s_nlit,
-                                                 int* sel_out, int* ninc_out, int* s_pw, long long* part) {
+                                                 const float* s_usel, const float* inv_rank, const uint16_t* s_lits,
+                                                 const int* s_nlit, int* sel_out, int* ninc_out, int* s_pw,
+                                                 long long* part) {
   const int64_t PW = (g.P + 31) / 32;
   if (g.list_cap > 0 && PW <= 16)
     resident_eval_lm_groups<INJECT, 16>(a, g, j, c_begin, idx0, stride, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel,
-                                        s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
+                                        inv_rank, s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
   else if (g.list_cap > 0 && PW <= 32)
     resident_eval_lm_groups<INJECT, 32>(a, g, j, c_begin, idx0, stride, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel,
-                                        s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
+                                        inv_rank, s_lits, s_nlit, sel_out, ninc_out, s_pw, part);
   else
     for (int idx = idx0; idx < n_own; idx += stride)
-      resident_eval<INJECT>(a, g, j, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, sel_out,
-                            ninc_out, s_pw, part);
+      resident_eval<INJECT>(a, g, j, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, inv_rank, s_lits, s_nlit,
+                            sel_out, ninc_out, s_pw, part);
 }
 
 // Phase A of the one-patch clauses idx0, idx0 + stride, ... (below n_own) on sample j, by
@@ -1584,6 +1624,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   int* s_slot_idx = (int*)(s_task_w + cpw * g.K);                 // [R] clause of a draw slot
   int* s_slot_k = s_slot_idx + R;                                 // [R] class of a draw slot
   uint32_t* s_rng = (uint32_t*)(s_slot_k + R);                    // [R][W][kPreGroups][4]
+  float* s_invr = (float*)(s_rng + (int64_t)R * g.W * kPreGroups * 4);  // [P+1] reservoir thresholds 1.0f / r
   unsigned long long my_updates = 0ull;
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
@@ -1599,6 +1640,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     if (g.P == 1) s_pw[j] = a.patch_w[c_begin + j];
   }
   for (int64_t j = threadIdx.x; j < g.K; j += blockDim.x) s_bias[j] = a.bias[j];
+  if (g.P > 1)
+    for (int64_t j = threadIdx.x; j <= g.P; j += blockDim.x) s_invr[j] = a.inv_rank[j];
   for (int j = 0; j < 2 && j < a.N; ++j) {
     stage_sample(a, g, j, j, s_x, s_y, threadIdx.x, blockDim.x);
     if (g.P > 1) stage_xt(a, g, j, j, s_xt, threadIdx.x, blockDim.x);
@@ -1638,8 +1681,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
       resident_eval_multi<INJECT>(a, g, 0, c_begin, wave, nwv, n_own, s_planes, s_w, s_drop, s_x, s_usel, s_sel, s_ninc,
                                   s_pw, s_part[0]);
     else
-      resident_eval_lm<INJECT>(a, g, 0, c_begin, wave, nwv, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit,
-                               s_sel, s_ninc, s_pw, s_part[0]);
+      resident_eval_lm<INJECT>(a, g, 0, c_begin, wave, nwv, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_invr, s_lits,
+                               s_nlit, s_sel, s_ninc, s_pw, s_part[0]);
   }
   __syncthreads();
   prof_last = __builtin_amdgcn_s_memrealtime();
@@ -1660,6 +1703,19 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   const int64_t cpw_g = (g.C + g.grid - 1) / g.grid + 1;
   const bool fused = g.coalesced && (cpw_g + cpp - 1) / cpp <= kFusedPasses;
   const long long bias_kk = (long long)s_bias[kk < g.K ? kk : 0];  // fused: class kk's bias (fixed for the launch)
+  // Several patches: phase A of sample i+1 takes passes of lm_ng clauses, one per wave of
+  // waves 1..; when that leaves two or more waves without a pass, those last waves
+  // (stage_waves) stage sample i+2 while the others evaluate.  Staging threads are
+  // [st_first, blockDim.x).  Decided from the geometry (g.threads is the launch's block
+  // size, and no workgroup owns more than ceil(C / grid) clauses), so that a specialised
+  // kernel keeps one of the two paths.
+  const int64_t pw_words = (g.P + 31) / 32;
+  const int lm_ng = g.list_cap > 0 && pw_words <= 16 ? 4 : (g.list_cap > 0 && pw_words <= 32 ? 2 : 1);
+  const int64_t own_max = (g.C + g.grid - 1) / g.grid;
+  const int lm_idle = (int)(g.threads / kWave - 1 - (own_max + lm_ng - 1) / lm_ng);
+  const int stage_waves = g.P > 1 && lm_idle >= 2 ? lm_idle : 0;
+  const int st_first = (nwv - (stage_waves ? stage_waves : nwv - 1)) * kWave;
+  const int st_count = (int)blockDim.x - st_first;
 
   for (int i = 0; i < a.N; ++i) {
     const uint64_t t = a.step0 + (uint64_t)i;
@@ -1767,23 +1823,33 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
             yq = a.Y[(int64_t)(i + 3) * g.K + (q - g.W)];
         }
       }
+      // Several patches: the waves without a pass of phase A (stage_waves) stage sample i+2
+      // meanwhile; without such waves, every wave stages it after phase A, its literal-major
+      // words read into registers before.
+      XtPre xpre;
+      if (g.P > 1 && !stage_waves && i + 2 < a.N)
+        xt_prefetch(a, g, i + 2, threadIdx.x - kWave, blockDim.x - kWave, &xpre);
       if (more) {
         if (g.P == 1)
           resident_eval_multi<INJECT>(a, g, i + 1, c_begin, wave - 1, nwv - 1, n_own, s_planes, s_w, s_drop, s_x, s_usel,
                                       s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
         else
           resident_eval_lm<INJECT>(a, g, i + 1, c_begin, wave - 1, nwv - 1, n_own, s_planes, s_w, s_drop, s_x, s_xt, s_usel,
-                                   s_lits, s_nlit, s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+                                   s_invr, s_lits, s_nlit, s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
       }
       if (a.profile == 2) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
-      if (i + 2 < a.N) {
+      if (i + 2 < a.N && (int)threadIdx.x >= st_first) {
         const int b3nn = (i + 2) % 3;
-        if (!early) stage_sample(a, g, i + 2, b3nn, s_x, s_y, threadIdx.x - kWave, blockDim.x - kWave);
+        const int st = (int)threadIdx.x - st_first;
+        if (!early) stage_sample(a, g, i + 2, b3nn, s_x, s_y, st, st_count);
         if (a.profile == 3) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
-        if (g.P > 1) stage_xt(a, g, i + 2, b2, s_xt, threadIdx.x - kWave, blockDim.x - kWave);
-        if (!INJECT)
-          precompute_draws(a, g, i + 2, b3nn, c_begin, n_own, s_usel, s_uq, s_uu, threadIdx.x - kWave,
-                           blockDim.x - kWave);
+        if (g.P > 1) {
+          if (stage_waves)
+            stage_xt(a, g, i + 2, b2, s_xt, st, st_count);
+          else
+            xt_commit(a, g, i + 2, b2, s_xt, st, st_count, xpre);
+        }
+        if (!INJECT) precompute_draws(a, g, i + 2, b3nn, c_begin, n_own, s_usel, s_uq, s_uu, st, st_count);
       }
       if (a.profile == 1) spec_ticks += __builtin_amdgcn_s_memrealtime() - spec_t0;
     }
@@ -1930,7 +1996,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         if (more)
           for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk)
             resident_eval<INJECT>(a, g, i + 1, c_begin, s_task_idx[tk], s_planes, s_w, s_drop, s_x, s_xt, s_usel,
-                                  s_lits, s_nlit, s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+                                  s_invr, s_lits, s_nlit, s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
       }
     } else {
       for (int tk = wave; tk < ntask; tk += nwv) {  // tasks round-robin over the waves
@@ -1949,8 +2015,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
           if (lane == 0) s_nlit[idx] = n;
         }
         if (more)
-          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_lits, s_nlit, s_sel + b2n * cpw,
-                                s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+          resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_invr, s_lits, s_nlit,
+                                s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
       }
     }
     YTM_PROF_MARK(5);
