@@ -193,7 +193,11 @@ def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=No
             f"kernel {ep['kernel_ms']:.1f}ms updates {ep['updates']} ({ep['updates'] / N:.2f}/sample) "
             f"feedback samples {ep['feedback']} evaluations {ep['evals']} workgroups {ep['wgs']} "
             f"kernel {KIND_NAMES.get(ep['kind'], ep['kind'])} wait {ep['wait']:.3f}")
-        if os.environ.get("YTM_TRAIN_PROFILE"):
+        if os.environ.get("YTM_TRAIN_PROFILE") == "4":
+            d = st["last_fit_draws"]
+            log(f"[bench]   counter-stream words per sample (lane draw sites): reservoir {d[0] / N:.0f} "
+                f"q-skip/update {d[1] / N:.0f} literal {d[2] / N:.0f}")
+        elif os.environ.get("YTM_TRAIN_PROFILE"):
             names = {0: ("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier", "step1-slowest-wave"),
                      3: ("stream", "drain", "decide", "apply")}.get(
                          ep["kind"], ("A", "barrier", "exchange", "barrier", "D", "barrier"))

@@ -105,6 +105,10 @@ typedef struct ytm_stats {
     int32_t last_fit_stream;     /* 1 when the last fit ran the streaming kernel (train_kind
                                     is then 3) */
     int32_t reserved;
+    uint64_t last_fit_draws[3];  /* with YTM_TRAIN_PROFILE=4: counter-stream words computed
+                                    by the last fit's training kernel, one per lane and draw
+                                    site (a Philox4x32-10 call): reservoir draws, Q-skip /
+                                    update draws, literal draws.  Zero otherwise */
 } ytm_stats;
 
 /* Thread-local description of the last failure. */

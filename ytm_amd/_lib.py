@@ -59,6 +59,7 @@ class YtmStats(ctypes.Structure):
         ("last_fit_evaluations", ctypes.c_uint64),
         ("last_fit_stream", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("last_fit_draws", ctypes.c_uint64 * 3),
     ]
 
 

@@ -228,6 +228,7 @@ class BaseTM:
         check(lib.ytm_get_stats(self._handle, ctypes.byref(st)))
         out = {name: getattr(st, name) for name, _ in st._fields_}
         out["last_fit_phase_us"] = list(out["last_fit_phase_us"])
+        out["last_fit_draws"] = list(out["last_fit_draws"])
         return out
 
     # ------------------------------------------------------------------ encode

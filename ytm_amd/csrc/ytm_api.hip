@@ -163,6 +163,12 @@ int ensure_slots(ytm_model* m, size_t bytes) {
   return YTM_OK;
 }
 
+// YTM_TRAIN_PROFILE: 0 off; 1-3 phase timings (TrainArgs::profile); 4 draw counts.
+int prof_level() {
+  const char* env = std::getenv("YTM_TRAIN_PROFILE");
+  return env ? std::max(0, std::atoi(env)) : 0;
+}
+
 int check_valid(const ytm_model* m) {
   if (m->invalid)
     return fail(YTM_EINVAL, "the model's state is a mix of samples after a training launch timed out; load a whole "
@@ -618,8 +624,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.slot_stride = slot_stride;
     a.cpw = cpw;
     a.rng_slots = rng_slots;
-    const char* prof_env = std::getenv("YTM_TRAIN_PROFILE");
-    a.profile = prof_env ? std::max(0, std::atoi(prof_env)) : 0;
+    a.profile = prof_level();
     const char* tt_env = std::getenv("YTM_TRAIN_TEST_TIMEOUT");  // test hook of the timeout path
     a.test_timeout = tt_env && std::atoi(tt_env) > 0;
     a.g = g;
@@ -653,6 +658,10 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   m->stats.last_fit_stream = kind == ytm::TrainKind::kStream;
   m->stats.last_fit_feedback_samples = kind == ytm::TrainKind::kStream ? cnt[12] : (uint64_t)count;
   m->stats.last_fit_evaluations = kind == ytm::TrainKind::kStream ? cnt[13] / (uint64_t)grid : (uint64_t)count;
+  const bool counted = prof_level() == 4;
+  m->stats.last_fit_draws[0] = counted ? cnt[14] : 0;
+  m->stats.last_fit_draws[1] = counted ? cnt[3] : 0;
+  m->stats.last_fit_draws[2] = counted ? cnt[15] : 0;
 #undef FIT_TRY
   m->stats.last_fit_wait_frac = cnt[2] ? (double)cnt[1] / (double)cnt[2] : 0.0;
   m->stats.train_kind = (int32_t)kind;

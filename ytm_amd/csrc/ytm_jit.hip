@@ -46,7 +46,10 @@ const char* kernel_name(TrainKind kind) {
 }
 
 std::string kernel_source(const Geom& g, TrainKind kind, bool inject) {
-  std::string s = "#include \"ytm_train.h\"\nnamespace ytm {\nstatic constexpr Geom kJitGeom = {\n";
+  // draw counting (YTM_TRAIN_PROFILE=4) only in the kernels of counting runs
+  const char* prof = std::getenv("YTM_TRAIN_PROFILE");
+  std::string s = std::string("#define YTM_COUNT_DRAWS ") + (prof && std::atoi(prof) == 4 ? "1" : "0") + "\n";
+  s += "#include \"ytm_train.h\"\nnamespace ytm {\nstatic constexpr Geom kJitGeom = {\n";
 #define YTM_GEOM_PRINT(type, name) \
   s += "  /* " #name " */ ";       \
   append_value(&s, (type)g.name);  \

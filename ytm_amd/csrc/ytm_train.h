@@ -29,6 +29,22 @@ namespace ytm {
 // (2 s), independent of how long one poll takes under contention.
 constexpr uint64_t kWaitTicks = 200000000ull;
 
+// The counter-stream words of a draw site (site_words).  With a.profile == 4 (counting
+// runs) the lanes that compute a site are added up per kind: counters[3] Q-skip / update
+// draws, [14] reservoir draws, [15] literal draws.  The counting is compiled in unless
+// YTM_COUNT_DRAWS is 0 (kernels compiled per model leave it out of runs that do not count).
+#ifndef YTM_COUNT_DRAWS
+#define YTM_COUNT_DRAWS 1
+#endif
+__device__ __forceinline__ U4 counted_site(const TrainArgs& a, uint64_t t, uint32_t c, uint32_t tag, uint32_t site) {
+  if (YTM_COUNT_DRAWS && a.profile == 4) {
+    const unsigned long long m = __ballot(1);
+    if ((int)(threadIdx.x & (kWave - 1)) == __ffsll((long long)m) - 1)
+      atomicAdd(&a.counters[tag == TAG_LIT ? 15 : (tag == TAG_SEL ? 14 : 3)], (unsigned long long)__popcll(m));
+  }
+  return site_words(a.seed, t, c, tag, site);
+}
+
 // Plane groups (4 planes each, most significant first) of the literal draws that the
 // resident kernel computes cooperatively ahead of applying an update.
 constexpr int kPreGroups = 3;
@@ -78,7 +94,7 @@ __device__ __forceinline__ uint32_t literal_draw_mask(const TrainArgs& a, const 
       const U4 z = (have_pre && grp < kPreGroups)
                        ? (pre ? U4{pre[grp * 4 + 0], pre[grp * 4 + 1], pre[grp * 4 + 2], pre[grp * 4 + 3]}
                               : U4{0u, 0u, 0u, 0u})
-                       : site_words(a.seed, t, (uint32_t)c, TAG_LIT, (uint32_t)((k * g.W + w) * 6 + grp));
+                       : counted_site(a, t, (uint32_t)c, TAG_LIT, (uint32_t)((k * g.W + w) * 6 + grp));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = 23 - 4 * grp - i;
@@ -114,7 +130,7 @@ __device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g,
           if (r <= R && inj[c * g.P + (r - 1)] < inv_rank[r]) lb = r;
         }
       } else {
-        const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
+        const U4 z = counted_site(a, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * gl + 1 + j;
@@ -395,7 +411,7 @@ __device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const flo
           if (r <= R && inj[c * g.P + (r - 1)] < inv_rank[r]) lb = r;
         }
       } else {
-        const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
+        const U4 z = counted_site(a, t, (uint32_t)c, TAG_SEL, (uint32_t)gl);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int r = 4 * gl + 1 + q;
@@ -496,7 +512,7 @@ __device__ int eval_select(const TrainArgs& a, const Geom& g, const float* inj, 
     else if (PRE)
       u = u_pre;
     else
-      u = uniform_from_word(site_words(a.seed, t, (uint32_t)c, TAG_SEL, 0u).x);
+      u = uniform_from_word(counted_site(a, t, (uint32_t)c, TAG_SEL, 0u).x);
     return u < 1.0f ? 0 : -1;  // 1.0f / 1
   } else {
     int cnt = 0;
@@ -578,7 +594,7 @@ __device__ FbOps decide(const TrainArgs& a, const Geom& g, const float* inj, int
     uq = pre_uq[k];
     uu = pre_uu[k];
   } else {
-    const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)k);
+    const U4 z = counted_site(a, t, (uint32_t)c, TAG_CK, (uint32_t)k);
     uq = uniform_from_word(z.x);
     uu = uniform_from_word(z.y);
   }
@@ -1206,10 +1222,56 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     YTM_PROF_MARK(3);
     if (s_abort) break;
 
-    // ---- D: feedback.  Decisions (weights updated in place) per clause, claimed
-    // dynamically; narrow clauses (W <= 32) are queued and their literal updates packed
-    // several to a wave, wide ones are updated right away by the deciding wave.
+    // ---- D: feedback.  Decisions (weights updated in place), claimed dynamically: lanes
+    // take (clause, class) pairs, kn classes per clause and 64 / kn clauses per claim
+    // (decide_pair), or a wave takes a clause when kn is above 32 (decide); a clause that
+    // changes is queued.  Narrow clauses (W <= 32) then have their literal updates packed
+    // several to a wave, wide ones a 64-word chunk per wave.
+    const int kn = g.coalesced ? (int)g.K : 1;
+    const int cpp = kWave / kn;
     for (;;) {
+      if (cpp < 2) break;  // decided a clause per wave below
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&s_next, cpp);
+      base = lane_value(base, 0);
+      if (base >= n_own) break;
+      const int jc = lane / kn, kk = lane - jc * kn;
+      const int idx = base + jc;
+      const bool valid = jc < cpp && idx < n_own;
+      const int ix = valid ? idx : base;  // idle lanes read a valid clause and discard it
+      const int64_t c = c_begin + ix;
+      const int64_t k = (g.coalesced ? 0 : c / g.per_bank) + kk;
+      float* wp = s_wg + (int64_t)ix * g.K + k;
+      const float wold = *wp;
+      float uq = 0.0f, uu = 0.0f;
+      if (!INJECT) {
+        const U4 z = counted_site(a, t, (uint32_t)c, TAG_CK, (uint32_t)k);
+        uq = uniform_from_word(z.x);
+        uu = uniform_from_word(z.y);
+      }
+      const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && a.drop[c] != 1u, s_sel[ix], s_ninc[ix], s_tgt[k],
+                                             s_prob[k], 1.0, wold, uq, uu);
+      if (po.t1a || po.t2) *wp = po.w_new;
+      const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
+      if ((b1a | b1b | bt2) == 0ull) continue;
+      const unsigned long long seg = (1ull << kn) - 1ull;
+      const int sh = jc * kn;
+      const unsigned long long m1a = valid ? (b1a >> sh) & seg : 0ull;
+      const unsigned long long m1b = valid ? (b1b >> sh) & seg : 0ull;
+      const unsigned long long m2 = valid ? (bt2 >> sh) & seg : 0ull;
+      const bool leader = (m1a | m1b | m2) != 0ull && kk == 0;
+      my_updates += (unsigned long long)__popcll(__ballot(leader));
+      if (leader) {
+        const int tk = atomicAdd(&s_ntask, 1);
+        s_task_idx[tk] = ix;
+        s_task_sb[tk] = 0;
+        s_task_m[tk * 3 + 0] = m1a;
+        s_task_m[tk * 3 + 1] = m1b;
+        s_task_m[tk * 3 + 2] = m2;
+      }
+    }
+    for (;;) {
+      if (cpp >= 2) break;  // decided in pairs above
       int idx = 0;
       if (lane == 0) idx = atomicAdd(&s_next, 1);
       idx = lane_value(idx, 0);
@@ -1299,10 +1361,10 @@ __device__ __forceinline__ void precompute_draws(const TrainArgs& a, const Geom&
     const int idx = j / per, r = j % per;
     const int64_t c = c_begin + idx;
     if (r == kn) {
-      s_usel[buf * a.cpw + idx] = uniform_from_word(site_words(a.seed, t, (uint32_t)c, TAG_SEL, 0u).x);
+      s_usel[buf * a.cpw + idx] = uniform_from_word(counted_site(a, t, (uint32_t)c, TAG_SEL, 0u).x);
     } else {
       const int64_t k = (g.coalesced ? 0 : c / g.per_bank) + r;
-      const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)k);
+      const U4 z = counted_site(a, t, (uint32_t)c, TAG_CK, (uint32_t)k);
       s_uq[((int64_t)buf * a.cpw + idx) * g.K + k] = uniform_from_word(z.x);
       s_uu[((int64_t)buf * a.cpw + idx) * g.K + k] = uniform_from_word(z.y);
     }
@@ -1961,7 +2023,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         const int64_t w = rem / npre;
         const int grp = rem % npre;
         const int64_t k = s_slot_k[sl];
-        const U4 z = site_words(a.seed, t, (uint32_t)(c_begin + s_slot_idx[sl]), TAG_LIT,
+        const U4 z = counted_site(a, t, (uint32_t)(c_begin + s_slot_idx[sl]), TAG_LIT,
                                 (uint32_t)((k * g.W + w) * 6 + grp));
         uint32_t* dst = s_rng + ((int64_t)sl * g.W + w) * (kPreGroups * 4) + grp * 4;
         dst[0] = z.x;
@@ -2276,7 +2338,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         // below 1.0f / 1
         bool sel = false;
         if (__any(fire)) {
-          const U4 z = site_words(a.seed, a.step0 + (uint64_t)s, (uint32_t)(c_begin + (own ? lane : 0)), TAG_SEL, 0u);
+          const U4 z = counted_site(a, a.step0 + (uint64_t)s, (uint32_t)(c_begin + (own ? lane : 0)), TAG_SEL, 0u);
           sel = fire && uniform_from_word(z.x) < 1.0f;
         }
         const unsigned long long smask = __ballot(sel);
@@ -2329,7 +2391,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         const int ix = valid ? idx : base;  // idle lanes read a valid clause and discard it
         const int64_t c = c_begin + ix;
         const float w0 = s_w[ix * K + kk];
-        const U4 z = site_words(a.seed, t, (uint32_t)c, TAG_CK, (uint32_t)kk);
+        const U4 z = counted_site(a, t, (uint32_t)c, TAG_CK, (uint32_t)kk);
         const PairOps po = decide_pair<false>(g, nullptr, c, kk, valid && s_drop[ix] == 0, s_selj[ix], s_ninc[ix],
                                               ct.tgt, ct.num, ct.den, w0, uniform_from_word(z.x),
                                               uniform_from_word(z.y));

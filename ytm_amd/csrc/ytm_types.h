@@ -92,7 +92,8 @@ struct TrainArgs {
   const float* inv_rank;     // [P + 1], inv_rank[r] = 1.0f / r
   unsigned long long* slots; // [N][slot_stride], zero on entry
   unsigned long long* counters;  // [0] updated clauses, [1] wait ticks, [2] kernel ticks, [4..11] phases,
-                                 // [12] feedback samples, [13] evaluations (streaming kernel)
+                                 // [12] feedback samples, [13] evaluations (streaming kernel); with
+                                 // profile 4, lane draws: [3] Q-skip/update, [14] reservoir, [15] literal
   int* err;                  // {1, sample, workgroup, count} when a bounded wait expires
   int64_t inject_block;
   uint64_t step0;
@@ -101,7 +102,7 @@ struct TrainArgs {
   int64_t slot_stride;       // slot words per sample: groups == 1 ? ks : (2 groups + 1) ks, ks = K rounded to 16
   int cpw;                   // max clauses owned by one workgroup
   int rng_slots;             // literal-draw slots precomputed per sample (resident kernel)
-  int profile;               // accumulate per-phase times into counters[4..11]
+  int profile;               // accumulate per-phase times into counters[4..11]; 4: count draws instead
   int test_timeout;          // test hook: class-sum waits never see their sums and expire at once
   Geom g;
 };
