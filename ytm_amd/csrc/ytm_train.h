@@ -219,17 +219,17 @@ __device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* li
 
 // Firing bitmap of a clause from its literal list (n literals, padded to a multiple of 8)
 // on the literal-major sample xt: acc (lane j: patch word j < PW, the all-patches mask)
-// AND-ed with the bitsets of the listed literals, 8 per step (two 8-byte reads of the
+// AND-ed with the bitsets of the listed literals, 16 per step (four 8-byte reads of the
 // list); stops once nothing fires.  When at least two groups of PW lanes fit in the wave,
-// each group walks its own runs of 8 literals and the groups' bitmaps are AND-ed at the
-// end, so one step covers 8 * (64 / PW) literals.  list must be 8-byte aligned.
+// each group walks its own runs of 16 literals and the groups' bitmaps are AND-ed at the
+// end, so one step covers 16 * (64 / PW) literals.  list must be 8-byte aligned.
 __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16_t* list, int n, const uint32_t* xt,
                                                      uint32_t acc) {
   const int lane = lane_id();
   const int PW = (int)((g.P + 31) / 32);
   const int NG = kWave / PW;  // lane groups of PW lanes
   if (NG >= 2) {
-    // Group q (lanes [q*PW, (q+1)*PW)) ANDs the literal runs 8q, 8q + 8*NG, ... into its own
+    // Group q (lanes [q*PW, (q+1)*PW)) ANDs the literal runs 16q, 16q + 16*NG, ... into its own
     // partial bitmap (lane q*PW + w: word w); a group whose partial is empty everywhere ends
     // the walk, and the groups' partials are AND-ed together at the end.
     const int q = lane / PW, w = lane - q * PW;
@@ -237,14 +237,18 @@ __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16
     // word w of the all-patches mask
     uint32_t part = in_group ? (w == PW - 1 && (g.P & 31) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu) : 0u;
     const unsigned long long gmask = PW >= 64 ? ~0ull : ((1ull << PW) - 1ull);
-    for (int j0 = 0; j0 < n; j0 += 8 * NG) {
-      const int j = j0 + 8 * q;
+    for (int j0 = 0; j0 < n; j0 += 16 * NG) {
+      const int j = j0 + 16 * q;
       if (in_group && j < n) {
+        // two runs of 8 per step, all 16 reads in flight together; without a second run the
+        // first is read twice (the AND is idempotent)
+        const int j1 = j + 8 < n ? j + 8 : j;
         const uint2 q0 = *(const uint2*)(list + j), q1 = *(const uint2*)(list + j + 4);
-        const uint32_t w8[4] = {q0.x, q0.y, q1.x, q1.y};
+        const uint2 q2 = *(const uint2*)(list + j1), q3 = *(const uint2*)(list + j1 + 4);
+        const uint32_t w8[8] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
         uint32_t v = 0xFFFFFFFFu;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 8; ++u) {
           v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)w];
           v &= xt[(w8[u] >> 16) * (uint32_t)PW + (uint32_t)w];
         }
@@ -265,17 +269,19 @@ __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16
     return lane < PW ? (r & acc) : 0u;
   }
   const int jl = lane < PW ? lane : 0;
-  for (int j = 0; j < n; j += 8) {
+  for (int j = 0; j < n; j += 16) {
+    const int j1 = j + 8 < n ? j + 8 : j;  // second run of the step (the first again if none)
     const uint2 q0 = *(const uint2*)(list + j), q1 = *(const uint2*)(list + j + 4);
-    const uint32_t w8[4] = {q0.x, q0.y, q1.x, q1.y};
+    const uint2 q2 = *(const uint2*)(list + j1), q3 = *(const uint2*)(list + j1 + 4);
+    const uint32_t w8[8] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
     uint32_t v = 0xFFFFFFFFu;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 8; ++u) {
       v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)jl];
       v &= xt[(w8[u] >> 16) * (uint32_t)PW + (uint32_t)jl];
     }
     acc &= v;
-    if ((j & 8) && !__any(acc != 0u)) break;  // every 16 literals: stop once nothing fires
+    if (!__any(acc != 0u)) break;  // every 16 literals: stop once nothing fires
   }
   return acc;
 }
@@ -380,19 +386,23 @@ __device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const flo
   const int nn = live ? n : 0;
   const int nmax = wave_max_i32(nn);
   const uint32_t jl = (uint32_t)(j < PW ? j : 0);
-  for (int s0 = 0; s0 < nmax; s0 += 8) {
+  for (int s0 = 0; s0 < nmax; s0 += 16) {
     if (s0 < nn) {
+      // two runs of 8 per step, all 16 reads in flight together; without a second run the
+      // first is read twice (the AND is idempotent)
+      const int s1 = s0 + 8 < nn ? s0 + 8 : s0;
       const uint2 q0 = *(const uint2*)(list + s0), q1 = *(const uint2*)(list + s0 + 4);
-      const uint32_t w8[4] = {q0.x, q0.y, q1.x, q1.y};
+      const uint2 q2 = *(const uint2*)(list + s1), q3 = *(const uint2*)(list + s1 + 4);
+      const uint32_t w8[8] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
       uint32_t v = 0xFFFFFFFFu;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 8; ++u) {
         v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + jl];
         v &= xt[(w8[u] >> 16) * (uint32_t)PW + jl];
       }
       acc &= v;
     }
-    if ((s0 & 8) && !__any(acc != 0u)) break;  // every 16 literals: stop once nothing fires anywhere
+    if (!__any(acc != 0u)) break;  // stop once nothing fires anywhere
   }
   const int pc = __popc(acc);
   const int incl = group_scan_add<S>(pc);
@@ -1103,136 +1113,185 @@ __device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const f
   }
 }
 
-// Clause state in global memory (L2/MALL resident across samples); any P.
+// Phase A of sample j over the workgroup's clauses with state in global memory, claimed
+// through *claim: selections and include counts into sel_out / ninc_out, the votes into
+// part.  xt: the literal-major sample (several patches), xe: the sample's words (one
+// patch: with mask_lds its LDS copy), masks: the LDS include masks (mask_lds).
+template <bool VANILLA, bool INJECT>
+__device__ __forceinline__ void global_phase_a(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int n_own,
+                                               int* claim, const uint16_t* s_lits, const int* s_nlit, int cap,
+                                               const uint32_t* xt, const uint32_t* xe, const uint32_t* s_mask,
+                                               int* sel_out, int* ninc_out, const float* s_wg, long long* part) {
+  const int lane = lane_id();
+  const uint64_t t = a.step0 + (uint64_t)j;
+  const float* inj = INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr;
+  // Clauses with bitmaps of at most 16 words go four to a wave (eval_select_lm_group).  Two
+  // to a wave (32-lane groups) lost on config 4: claims of two clauses balance the waves
+  // worse (its phase A + barrier went from 10.8 to 11.5 us per sample).
+  const bool grouped = !VANILLA && literal_major(g) && cap > 0 && (g.P + 31) / 32 <= 16;
+  if (grouped) {
+    global_eval_lm_groups<INJECT, 16>(a, g, inj, t, c_begin, n_own, claim, s_lits, s_nlit, xt, sel_out, ninc_out, s_wg,
+                                      part, a.inv_rank);
+    return;
+  }
+  for (;;) {
+    int idx = 0;
+    if (lane == 0) idx = atomicAdd(claim, 1);
+    idx = lane_value(idx, 0);
+    if (idx >= n_own) break;
+    const int64_t c = c_begin + idx;
+    int ninc;
+    const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : a.planes + (c * g.np + g.np - 1) * g.W;
+    const int sel = (!VANILLA && literal_major(g))
+                        ? eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * cap,
+                                                 cap > 0 ? s_nlit[idx] : 0, cap, xt, a.drop[c] == 1u, &ninc, a.inv_rank)
+                        : eval_select<VANILLA, INJECT>(a, g, inj, c, t, m, xe, a.drop[c] == 1u, -1.0f, &ninc);
+    if (lane == 0) {
+      sel_out[idx] = sel;
+      ninc_out[idx] = ninc;
+    }
+    if (sel >= 0) add_partial(a, g, part, c, s_wg + (int64_t)idx * g.K);
+  }
+}
+
+// Clause state in global memory (L2/MALL resident across samples); any P.  A software
+// pipeline over samples, like the resident kernel's; per sample i:
+//   1. wave 0 adds the patch weights of sample i's selections (select_active,
+//      kernel.cu:305) and publishes its partial class sums; then every wave stages sample
+//      i+1 (its literal-major copy; with mask_lds its words) into LDS.
+//   2. wave 0 waits for sample i's totals and derives the targets (phases B/C); the other
+//      waves evaluate sample i+1 with the current state (phase A, speculative).
+//   3. D: the feedback decisions of sample i (clause_update, kernel.cu:531-613) take
+//      (clause, class) pairs, 64 / K clauses per claim (decide_pair), or a wave per clause
+//      when K is above 32 (decide); a clause that changes takes back its speculative votes
+//      for sample i+1 and is queued.  Then its literal updates: narrow clauses (W <= 32)
+//      several to a wave, wide ones a 64-word chunk per wave.
+//   4. the updated clauses rebuild their literal lists and are evaluated again for sample
+//      i+1, so the result is exactly the sequential one.
+// Phase A of sample i and its re-evaluations are over before sample i+1 is staged, so one
+// literal-major buffer serves; the words of samples i and i+1 (mask_lds) take two.
 template <bool VANILLA, bool INJECT>
 __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom& g) {
   extern __shared__ long long dyn_lds[];
-  __shared__ long long s_part[64];
+  __shared__ long long s_part[2][64];  // partial class sums by sample parity
   __shared__ int s_tgt[64];
   __shared__ double s_prob[64];
-  __shared__ int s_next;
+  __shared__ int s_next_a, s_next_d;  // clause claims of phase A and of the decisions
   __shared__ int s_abort;
+  __shared__ int s_ntask;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
+  const int nwv = (int)(blockDim.x / kWave);
   const int G = gridDim.x, wg = blockIdx.x;
   const int64_t c_begin = g.C * wg / G, c_end = g.C * (wg + 1) / G;
   const int n_own = (int)(c_end - c_begin);
-  __shared__ int s_ntask;
+  const int cpw = a.cpw;
   unsigned long long* s_task_m = (unsigned long long*)dyn_lds;  // [cpw][3] feedback masks
-  int* s_sel = (int*)(s_task_m + 3 * a.cpw);                   // [cpw]
-  int* s_ninc = s_sel + a.cpw;                                 // [cpw]
-  int* s_task_idx = s_ninc + a.cpw;                            // [cpw]
-  int* s_task_sb = s_task_idx + a.cpw;                         // [cpw] (zero: no precomputed draws)
+  int* s_sel = (int*)(s_task_m + 3 * cpw);                     // [2][cpw] by sample parity
+  int* s_ninc = s_sel + 2 * cpw;                               // [2][cpw]
+  int* s_task_idx = s_ninc + 2 * cpw;                          // [cpw]
+  int* s_task_sb = s_task_idx + cpw;                           // [cpw] (zero: no precomputed draws)
   const int cap = VANILLA ? 0 : g.list_cap;                    // literal list capacity
-  int* s_nlit = s_task_sb + a.cpw;                             // [cpw] include counts (cap > 0)
-  uint16_t* s_lits = (uint16_t*)(s_nlit + (cap > 0 ? 2 * ((a.cpw + 1) / 2) : 0));  // [cpw][cap] literal lists
-  uint32_t* s_xt = (uint32_t*)(s_lits + (int64_t)a.cpw * cap);  // [L][PW] when literal_major_lds(g)
+  int* s_nlit = s_task_sb + cpw;                               // [cpw] include counts (cap > 0)
+  uint16_t* s_lits = (uint16_t*)(s_nlit + (cap > 0 ? 2 * ((cpw + 1) / 2) : 0));  // [cpw][cap] literal lists
+  uint32_t* s_xt = (uint32_t*)(s_lits + (int64_t)cpw * cap);  // [L][PW] when literal_major_lds(g)
   const int64_t cw = (int64_t)g.np * g.W;
   const int64_t xt_words = literal_major(g) ? g.L * ((g.P + 31) / 32) : 0;
   // mask_lds (one patch): the own clauses' include masks [cpw][W], kept current by the
-  // literal updates, and the current sample [W]
+  // literal updates, and the words of samples i and i+1 [2][W]
   uint32_t* s_mask = s_xt + (literal_major_lds(g) ? xt_words : 0);
-  uint32_t* s_xs = s_mask + (g.mask_lds ? (int64_t)a.cpw * g.W : 0);
-  float* s_wg = (float*)(s_xs + (g.mask_lds ? g.W : 0));  // the own clauses' weights [cpw][K]
+  uint32_t* s_xs = s_mask + (g.mask_lds ? (int64_t)cpw * g.W : 0);
+  float* s_wg = (float*)(s_xs + (g.mask_lds ? 2 * g.W : 0));  // the own clauses' weights [cpw][K]
+  const bool lm = !VANILLA && literal_major(g);
   unsigned long long my_updates = 0ull;
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
   const bool prof = a.profile && wave == 0;
   uint64_t prof_acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   uint64_t prof_last = t_kernel;
-  if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
-  if (threadIdx.x == 0) s_abort = 0;
+  if (threadIdx.x < 128) (&s_part[0][0])[threadIdx.x] = 0;
+  if (threadIdx.x == 0) {
+    s_abort = 0;
+    s_next_a = 0;
+  }
   for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) s_wg[j] = a.weights[c_begin * g.K + j];
   if (g.mask_lds)  // include masks of the own clauses (visible after the first barrier below)
-    for (int idx = wave; idx < n_own; idx += (int)(blockDim.x / kWave))
+    for (int idx = wave; idx < n_own; idx += nwv)
       for (int64_t w = lane; w < g.W; w += kWave)
         s_mask[(int64_t)idx * g.W + w] = a.planes[(c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W + w];
   if (cap > 0)  // literal lists of the own clauses (visible after the first barrier below)
-    for (int idx = wave; idx < n_own; idx += (int)(blockDim.x / kWave)) {
+    for (int idx = wave; idx < n_own; idx += nwv) {
       const int n = build_literal_list(g, a.planes + (c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W,
                                        s_lits + (int64_t)idx * cap, cap);
       if (lane == 0) s_nlit[idx] = n;
     }
-
-  for (int i = 0; i < a.N; ++i) {
+  // The LDS copy of sample j (threads [first, first + count)): literal-major words, or with
+  // mask_lds the words into buffer j & 1.  The sample of phase A / re-evaluation: xt_of,
+  // xe_of.
+  auto stage = [&](int j, int first, int count) {
+    if (g.mask_lds) copy_to_lds(s_xs + (int64_t)(j & 1) * g.W, a.X + (int64_t)j * g.W, g.W, first, count);
+    if (lm && literal_major_lds(g)) copy_to_lds(s_xt, a.XT + (int64_t)j * xt_words, xt_words, first, count);
+  };
+  auto xt_of = [&](int j) -> const uint32_t* {
+    return !lm ? nullptr : (literal_major_lds(g) ? s_xt : a.XT + (int64_t)j * xt_words);
+  };
+  auto xe_of = [&](int j) -> const uint32_t* {
+    return g.mask_lds ? s_xs + (int64_t)(j & 1) * g.W : a.X + (int64_t)j * g.P * g.W;
+  };
+  const int kn = g.coalesced ? (int)g.K : 1;
+  const int cpp = kWave / kn;
+  // i = -1 is the prologue: every wave stages sample 0 and takes part in its phase A
+  for (int i = -1; i < a.N; ++i) {
     const uint64_t t = a.step0 + (uint64_t)i;
-    const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
-    const uint32_t* xe = a.X + (int64_t)i * g.P * g.W;
-    if (g.mask_lds) {
-      copy_to_lds(s_xs, xe, g.W, threadIdx.x, blockDim.x);
-      xe = s_xs;
-    }
-    const uint32_t* xt = nullptr;  // literal-major sample
-    if (!VANILLA && literal_major(g)) {
-      xt = a.XT + (int64_t)i * xt_words;
-      if (literal_major_lds(g)) {
-        copy_to_lds(s_xt, xt, xt_words, threadIdx.x, blockDim.x);
-        xt = s_xt;
-      }
-    }
-    if (threadIdx.x == 0) s_next = 0;
-    __syncthreads();
+    const float* inj = INJECT && i >= 0 ? a.inject + (int64_t)i * a.inject_block : nullptr;
+    const int b = i & 1, bn = b ^ 1;
+    const bool more = i + 1 < a.N;
+    int* sel_i = s_sel + b * cpw;
+    int* ninc_i = s_ninc + b * cpw;
+    int* sel_n = s_sel + bn * cpw;
+    int* ninc_n = s_ninc + bn * cpw;
 
-    // ---- A: evaluation, reservoir selection, partial class sums
-    // Clauses with bitmaps of at most 16 words go four to a wave (eval_select_lm_group).  Two
-    // to a wave (32-lane groups) lost on config 4: claims of two clauses balance the waves
-    // worse (its phase A + barrier went from 10.8 to 11.5 us per sample).
-    const bool grouped = !VANILLA && literal_major(g) && cap > 0 && (g.P + 31) / 32 <= 16;
-    if (grouped)
-      global_eval_lm_groups<INJECT, 16>(a, g, inj, t, c_begin, n_own, &s_next, s_lits, s_nlit, xt, s_sel, s_ninc, s_wg,
-                                        s_part, a.inv_rank);
-    for (;;) {
-      if (grouped) break;  // done above
-      int idx = 0;
-      if (lane == 0) idx = atomicAdd(&s_next, 1);
-      idx = lane_value(idx, 0);
-      if (idx >= n_own) break;
-      const int64_t c = c_begin + idx;
-      int ninc;
-      const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : a.planes + (c * g.np + g.np - 1) * g.W;
-      const int sel = (!VANILLA && literal_major(g))
-                          ? eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * cap,
-                                                   cap > 0 ? s_nlit[idx] : 0, cap, xt, a.drop[c] == 1u, &ninc, a.inv_rank)
-                          : eval_select<VANILLA, INJECT>(a, g, inj, c, t, m, xe, a.drop[c] == 1u, -1.0f, &ninc);
-      if (lane == 0) {
-        s_sel[idx] = sel;
-        s_ninc[idx] = ninc;
-      }
-      if (sel >= 0) add_partial(a, g, s_part, c, s_wg + (int64_t)idx * g.K);
-    }
-    YTM_PROF_MARK(0);
-    __syncthreads();
-    YTM_PROF_MARK(1);
-
-    // ---- B + C; wave 0 first adds the patch weights of the sample's selections (select_active,
-    // kernel.cu:305), deferred out of phase A so that no evaluation waits on these atomics
-    if (wave == 0) {
+    // ---- 1: patch weights and publish of sample i; staging of sample i+1
+    if (i >= 0 && wave == 0) {
       for (int idx = lane; idx < n_own; idx += kWave) {
-        const int sl = s_sel[idx];
+        const int sl = sel_i[idx];
         if (sl >= 0) atomicAdd(&a.patch_w[(c_begin + idx) * g.P + sl], 1);
       }
-      exchange_class_sums(a, g, i, a.Y + (int64_t)i * g.K, a.bias, s_part, s_tgt, s_prob, &s_abort, &wait_ticks);
+      exchange_publish(a, g, i, s_part[b]);
+      if (lane == 0) {
+        s_next_a = 0;
+        s_next_d = 0;
+        s_ntask = 0;
+      }
     }
-    YTM_PROF_MARK(2);
-    if (threadIdx.x == 0) {
-      s_next = 0;
-      s_ntask = 0;
+    if (more) stage(i + 1, threadIdx.x, blockDim.x);
+    __syncthreads();
+    YTM_PROF_MARK(0);
+
+    // ---- 2: the totals of sample i (wave 0); speculative phase A of sample i+1 (the others)
+    if (i >= 0 && wave == 0) {
+      long long S = 0;
+      if (exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part[b], &S, &s_abort, &wait_ticks) &&
+          lane < g.K)
+        class_targets(g, lane, S + (long long)a.bias[lane], a.Y + (int64_t)i * g.K, s_tgt, s_prob);
+      YTM_PROF_MARK(1);
+    } else if (more) {
+      global_phase_a<VANILLA, INJECT>(a, g, i + 1, c_begin, n_own, &s_next_a, s_lits, s_nlit, cap, xt_of(i + 1),
+                                      xe_of(i + 1), s_mask, sel_n, ninc_n, s_wg, s_part[bn]);
     }
     __syncthreads();
-    YTM_PROF_MARK(3);
+    if (i < 0) {
+      prof_last = __builtin_amdgcn_s_memrealtime();
+      continue;
+    }
+    YTM_PROF_MARK(2);
     if (s_abort) break;
 
-    // ---- D: feedback.  Decisions (weights updated in place), claimed dynamically: lanes
-    // take (clause, class) pairs, kn classes per clause and 64 / kn clauses per claim
-    // (decide_pair), or a wave takes a clause when kn is above 32 (decide); a clause that
-    // changes is queued.  Narrow clauses (W <= 32) then have their literal updates packed
-    // several to a wave, wide ones a 64-word chunk per wave.
-    const int kn = g.coalesced ? (int)g.K : 1;
-    const int cpp = kWave / kn;
+    // ---- 3: decisions of sample i
     for (;;) {
       if (cpp < 2) break;  // decided a clause per wave below
       int base = 0;
-      if (lane == 0) base = atomicAdd(&s_next, cpp);
+      if (lane == 0) base = atomicAdd(&s_next_d, cpp);
       base = lane_value(base, 0);
       if (base >= n_own) break;
       const int jc = lane / kn, kk = lane - jc * kn;
@@ -1249,7 +1308,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         uq = uniform_from_word(z.x);
         uu = uniform_from_word(z.y);
       }
-      const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && a.drop[c] != 1u, s_sel[ix], s_ninc[ix], s_tgt[k],
+      const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && a.drop[c] != 1u, sel_i[ix], ninc_i[ix], s_tgt[k],
                                              s_prob[k], 1.0, wold, uq, uu);
       if (po.t1a || po.t2) *wp = po.w_new;
       const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
@@ -1259,7 +1318,11 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       const unsigned long long m1a = valid ? (b1a >> sh) & seg : 0ull;
       const unsigned long long m1b = valid ? (b1b >> sh) & seg : 0ull;
       const unsigned long long m2 = valid ? (bt2 >> sh) & seg : 0ull;
-      const bool leader = (m1a | m1b | m2) != 0ull && kk == 0;
+      const bool changes = (m1a | m1b | m2) != 0ull;
+      // a changed clause takes back the votes it cast for sample i+1 with its old weights
+      if (more && changes && sel_n[ix] >= 0)
+        atomicAdd((unsigned long long*)&s_part[bn][k], (unsigned long long)(-(long long)wold));
+      const bool leader = changes && kk == 0;
       my_updates += (unsigned long long)__popcll(__ballot(leader));
       if (leader) {
         const int tk = atomicAdd(&s_ntask, 1);
@@ -1273,14 +1336,18 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     for (;;) {
       if (cpp >= 2) break;  // decided in pairs above
       int idx = 0;
-      if (lane == 0) idx = atomicAdd(&s_next, 1);
+      if (lane == 0) idx = atomicAdd(&s_next_d, 1);
       idx = lane_value(idx, 0);
       if (idx >= n_own) break;
       const int64_t c = c_begin + idx;
       if (a.drop[c] == 1u) continue;
-      const FbOps ops = decide<INJECT, false>(a, g, inj, c, t, s_sel[idx], s_ninc[idx], s_tgt, s_prob,
+      const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
+      const float wold = s_wg[(int64_t)idx * g.K + kp];
+      const FbOps ops = decide<INJECT, false>(a, g, inj, c, t, sel_i[idx], ninc_i[idx], s_tgt, s_prob,
                                               s_wg + (int64_t)idx * g.K, nullptr, nullptr);
       if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
+      if (more && sel_n[idx] >= 0 && (g.coalesced ? lane < g.K : lane == 0))
+        atomicAdd((unsigned long long*)&s_part[bn][kp], (unsigned long long)(-(long long)wold));
       if (lane == 0) {
         ++my_updates;
         const int tk = atomicAdd(&s_ntask, 1);
@@ -1292,14 +1359,15 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       }
     }
     __syncthreads();
+    YTM_PROF_MARK(3);
     {
       const int ntask = s_ntask;
-      const int nwv = (int)(blockDim.x / kWave);
+      const uint32_t* xe = xe_of(i);  // sample i's words, for the literal updates
       if (g.W <= 32) {
         // narrow clauses: up to 64 / W queued updates per wave at once
         const int per = tasks_per_wave(g, ntask, nwv);
         for (int tk0 = wave * per; tk0 < ntask; tk0 += nwv * per)
-          apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb, s_sel,
+          apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb, sel_i,
                               a.planes + c_begin * cw, xe, nullptr, 0, g.mask_lds ? s_mask : nullptr);
       } else {
         // wide clauses: (update, 64-word chunk) items over all waves; the chunks of one
@@ -1309,23 +1377,44 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
           const int tk = item / nchunk, ch = item - tk * nchunk;
           const int idx = s_task_idx[tk];
           const FbOps ops{s_task_m[tk * 3 + 0], s_task_m[tk * 3 + 1], s_task_m[tk * 3 + 2]};
-          apply_ops<INJECT>(a, g, inj, c_begin + idx, t, s_sel[idx], ops, a.planes + (c_begin + idx) * cw, xe, nullptr,
+          apply_ops<INJECT>(a, g, inj, c_begin + idx, t, sel_i[idx], ops, a.planes + (c_begin + idx) * cw, xe, nullptr,
                             g.mask_lds ? s_mask + (int64_t)idx * g.W : nullptr, (int64_t)ch * kWave,
                             (int64_t)(ch + 1) * kWave);
         }
       }
     }
-    YTM_PROF_MARK(4);
     __syncthreads();
-    if (cap > 0) {  // the literal lists of the updated clauses (visible after the next barrier)
+    YTM_PROF_MARK(4);
+
+    // ---- 4: the updated clauses' literal lists, and their phase A of sample i+1 again
+    {
       const int ntask = s_ntask;
-      for (int tk = wave; tk < ntask; tk += (int)(blockDim.x / kWave)) {
+      const uint64_t tn = t + 1;
+      const float* injn = INJECT && more ? a.inject + (int64_t)(i + 1) * a.inject_block : nullptr;
+      for (int tk = wave; tk < ntask; tk += nwv) {
         const int idx = s_task_idx[tk];
-        const int n = build_literal_list(g, a.planes + (c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W,
-                                         s_lits + (int64_t)idx * cap, cap);
-        if (lane == 0) s_nlit[idx] = n;
+        const int64_t c = c_begin + idx;
+        const uint32_t* top = a.planes + c * cw + (int64_t)(g.np - 1) * g.W;
+        if (cap > 0) {
+          const int n = build_literal_list(g, top, s_lits + (int64_t)idx * cap, cap);
+          if (lane == 0) s_nlit[idx] = n;
+        }
+        if (!more) continue;
+        int ninc;
+        const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : top;
+        const int sel = lm ? eval_select_lm<INJECT>(a, g, injn, c, tn, m, s_lits + (int64_t)idx * cap,
+                                                    cap > 0 ? s_nlit[idx] : 0, cap, xt_of(i + 1), a.drop[c] == 1u,
+                                                    &ninc, a.inv_rank)
+                           : eval_select<VANILLA, INJECT>(a, g, injn, c, tn, m, xe_of(i + 1), a.drop[c] == 1u, -1.0f,
+                                                          &ninc);
+        if (lane == 0) {
+          sel_n[idx] = sel;
+          ninc_n[idx] = ninc;
+        }
+        if (sel >= 0) add_partial(a, g, s_part[bn], c, s_wg + (int64_t)idx * g.K);
       }
     }
+    __syncthreads();
     YTM_PROF_MARK(5);
   }
   __syncthreads();
