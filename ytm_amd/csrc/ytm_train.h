@@ -1064,7 +1064,7 @@ template <bool INJECT, int S>
 __device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const float* inj, uint64_t t, int64_t c_begin,
                                       int n_own, int* s_next, const uint16_t* s_lits, const int* s_nlit,
                                       const uint32_t* xt, int* s_sel, int* s_ninc, const float* s_wg, long long* s_part,
-                                      const float* inv_rank) {
+                                      const float* inv_rank, const int* s_drop) {
   constexpr int NG = kWave / S;
   const int lane = lane_id();
   const int q = lane / S, jj = lane & (S - 1);
@@ -1081,7 +1081,7 @@ __device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const f
     const bool listed = in && nl <= cap;
     const int64_t c = c_begin + ix;
     const int sel = eval_select_lm_group<INJECT, S>(a, g, inj, t, c, listed, s_lits + (int64_t)ix * cap, nl, xt,
-                                                    a.drop[c] == 1u, inv_rank);
+                                                    s_drop[ix] != 0, inv_rank);
     if (listed) {
       if (jj == 0) {
         s_sel[idx] = sel;
@@ -1103,7 +1103,7 @@ __device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const f
       int ninc;
       const uint32_t* m = a.planes + (c2 * g.np + g.np - 1) * g.W;
       const int sel2 = eval_select_lm<INJECT>(a, g, inj, c2, t, m, s_lits + (int64_t)i2 * cap, s_nlit[i2], cap, xt,
-                                              a.drop[c2] == 1u, &ninc, inv_rank);
+                                              s_drop[i2] != 0, &ninc, inv_rank);
       if (lane == 0) {
         s_sel[i2] = sel2;
         s_ninc[i2] = ninc;
@@ -1121,7 +1121,8 @@ template <bool VANILLA, bool INJECT>
 __device__ __forceinline__ void global_phase_a(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int n_own,
                                                int* claim, const uint16_t* s_lits, const int* s_nlit, int cap,
                                                const uint32_t* xt, const uint32_t* xe, const uint32_t* s_mask,
-                                               int* sel_out, int* ninc_out, const float* s_wg, long long* part) {
+                                               int* sel_out, int* ninc_out, const float* s_wg, long long* part,
+                                               const float* inv_rank, const int* s_drop) {
   const int lane = lane_id();
   const uint64_t t = a.step0 + (uint64_t)j;
   const float* inj = INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr;
@@ -1131,7 +1132,7 @@ __device__ __forceinline__ void global_phase_a(const TrainArgs& a, const Geom& g
   const bool grouped = !VANILLA && literal_major(g) && cap > 0 && (g.P + 31) / 32 <= 16;
   if (grouped) {
     global_eval_lm_groups<INJECT, 16>(a, g, inj, t, c_begin, n_own, claim, s_lits, s_nlit, xt, sel_out, ninc_out, s_wg,
-                                      part, a.inv_rank);
+                                      part, inv_rank, s_drop);
     return;
   }
   for (;;) {
@@ -1144,8 +1145,8 @@ __device__ __forceinline__ void global_phase_a(const TrainArgs& a, const Geom& g
     const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : a.planes + (c * g.np + g.np - 1) * g.W;
     const int sel = (!VANILLA && literal_major(g))
                         ? eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * cap,
-                                                 cap > 0 ? s_nlit[idx] : 0, cap, xt, a.drop[c] == 1u, &ninc, a.inv_rank)
-                        : eval_select<VANILLA, INJECT>(a, g, inj, c, t, m, xe, a.drop[c] == 1u, -1.0f, &ninc);
+                                                 cap > 0 ? s_nlit[idx] : 0, cap, xt, s_drop[idx] != 0, &ninc, inv_rank)
+                        : eval_select<VANILLA, INJECT>(a, g, inj, c, t, m, xe, s_drop[idx] != 0, -1.0f, &ninc);
     if (lane == 0) {
       sel_out[idx] = sel;
       ninc_out[idx] = ninc;
@@ -1202,6 +1203,9 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   uint32_t* s_mask = s_xt + (literal_major_lds(g) ? xt_words : 0);
   uint32_t* s_xs = s_mask + (g.mask_lds ? (int64_t)cpw * g.W : 0);
   float* s_wg = (float*)(s_xs + (g.mask_lds ? 2 * g.W : 0));  // the own clauses' weights [cpw][K]
+  int* s_drop = (int*)(s_wg + (int64_t)cpw * g.K);              // [cpw] dropped (1) or not
+  // several patches: the reservoir thresholds 1.0f / r, r = 0..P (a.inv_rank)
+  float* s_invr = (float*)(s_drop + cpw);
   const bool lm = !VANILLA && literal_major(g);
   unsigned long long my_updates = 0ull;
   uint64_t wait_ticks = 0;
@@ -1215,6 +1219,9 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     s_next_a = 0;
   }
   for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) s_wg[j] = a.weights[c_begin * g.K + j];
+  for (int j = threadIdx.x; j < n_own; j += blockDim.x) s_drop[j] = a.drop[c_begin + j] == 1u;
+  if (g.P > 1)
+    for (int64_t j = threadIdx.x; j <= g.P; j += blockDim.x) s_invr[j] = a.inv_rank[j];
   if (g.mask_lds)  // include masks of the own clauses (visible after the first barrier below)
     for (int idx = wave; idx < n_own; idx += nwv)
       for (int64_t w = lane; w < g.W; w += kWave)
@@ -1277,7 +1284,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       YTM_PROF_MARK(1);
     } else if (more) {
       global_phase_a<VANILLA, INJECT>(a, g, i + 1, c_begin, n_own, &s_next_a, s_lits, s_nlit, cap, xt_of(i + 1),
-                                      xe_of(i + 1), s_mask, sel_n, ninc_n, s_wg, s_part[bn]);
+                                      xe_of(i + 1), s_mask, sel_n, ninc_n, s_wg, s_part[bn], s_invr, s_drop);
     }
     __syncthreads();
     if (i < 0) {
@@ -1308,7 +1315,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         uq = uniform_from_word(z.x);
         uu = uniform_from_word(z.y);
       }
-      const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && a.drop[c] != 1u, sel_i[ix], ninc_i[ix], s_tgt[k],
+      const PairOps po = decide_pair<INJECT>(g, inj, c, k, valid && s_drop[ix] == 0, sel_i[ix], ninc_i[ix], s_tgt[k],
                                              s_prob[k], 1.0, wold, uq, uu);
       if (po.t1a || po.t2) *wp = po.w_new;
       const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
@@ -1340,7 +1347,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       idx = lane_value(idx, 0);
       if (idx >= n_own) break;
       const int64_t c = c_begin + idx;
-      if (a.drop[c] == 1u) continue;
+      if (s_drop[idx]) continue;
       const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
       const float wold = s_wg[(int64_t)idx * g.K + kp];
       const FbOps ops = decide<INJECT, false>(a, g, inj, c, t, sel_i[idx], ninc_i[idx], s_tgt, s_prob,
@@ -1403,9 +1410,9 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         int ninc;
         const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : top;
         const int sel = lm ? eval_select_lm<INJECT>(a, g, injn, c, tn, m, s_lits + (int64_t)idx * cap,
-                                                    cap > 0 ? s_nlit[idx] : 0, cap, xt_of(i + 1), a.drop[c] == 1u,
-                                                    &ninc, a.inv_rank)
-                           : eval_select<VANILLA, INJECT>(a, g, injn, c, tn, m, xe_of(i + 1), a.drop[c] == 1u, -1.0f,
+                                                    cap > 0 ? s_nlit[idx] : 0, cap, xt_of(i + 1), s_drop[idx] != 0,
+                                                    &ninc, s_invr)
+                           : eval_select<VANILLA, INJECT>(a, g, injn, c, tn, m, xe_of(i + 1), s_drop[idx] != 0, -1.0f,
                                                           &ninc);
         if (lane == 0) {
           sel_n[idx] = sel;
