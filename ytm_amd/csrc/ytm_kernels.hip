@@ -401,8 +401,14 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
 // clauses do not vote).  Lanes < K sum the weights of the firing clauses exactly.
 constexpr int64_t kScoreLmChunk = 4096;
 constexpr int kScoreListCap = 256;
+// Block size: 16 waves when the sample's literal-major copy is large (it is staged once per
+// block, and its LDS limits the blocks per CU, so only large blocks keep enough waves on a
+// CU to hide the latency of each clause's list reads: config 4, 64 KB, 1.9x), else 4
+// (config 3, 13 KB: 256 threads are 19% faster than 1024).
+constexpr int kScoreLmThreads = 1024;
+inline int score_lm_threads(const Geom& g) { return (g.L * ((g.P + 31) / 32)) * 4 > 32 * 1024 ? 1024 : 256; }
 
-__global__ __launch_bounds__(256) void score_lm_kernel(const uint32_t* __restrict__ planes,
+__global__ __launch_bounds__(kScoreLmThreads) void score_lm_kernel(const uint32_t* __restrict__ planes,
                                                        const uint16_t* __restrict__ lists,
                                                        const int32_t* __restrict__ nlit, const float* __restrict__ w,
                                                        const uint32_t* __restrict__ XT, int64_t N, Geom g,
@@ -589,7 +595,7 @@ __global__ __launch_bounds__(256) void tile_kernel(const uint32_t* __restrict__ 
 // clause's literal list when it has one).  MODE 0: out[e][c] = some patch fires;
 // MODE 1: out[e][c][p]; MODE 2: out[e][c][j] with bit b = patch 32j + b (0 beyond P).
 template <int MODE>
-__global__ __launch_bounds__(256) void transform_lm_kernel(const uint32_t* __restrict__ planes,
+__global__ __launch_bounds__(kScoreLmThreads) void transform_lm_kernel(const uint32_t* __restrict__ planes,
                                                            const uint16_t* __restrict__ lists,
                                                            const int32_t* __restrict__ nlit,
                                                            const uint32_t* __restrict__ XT, int64_t N, Geom g,
@@ -878,7 +884,8 @@ hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_
   build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
   const int64_t blocks = N * ((g.C + kScoreLmChunk - 1) / kScoreLmChunk);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
-  score_lm_kernel<<<grid, 256, (size_t)(g.L * ((g.P + 31) / 32)) * 4, s>>>(planes, lists, nlit, w, XT, N, g, acc);
+  score_lm_kernel<<<grid, score_lm_threads(g), (size_t)(g.L * ((g.P + 31) / 32)) * 4, s>>>(planes, lists, nlit, w, XT,
+                                                                                         N, g, acc);
   return hipGetLastError();
 }
 
@@ -985,11 +992,11 @@ hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64
   const int grid = blocks < 65536 ? (int)blocks : 65536;
   const size_t lds = (size_t)(g.L * ((g.P + 31) / 32)) * 4;
   if (mode == 0)
-    transform_lm_kernel<0><<<grid, 256, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+    transform_lm_kernel<0><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, XT, N, g, out);
   else if (mode == 1)
-    transform_lm_kernel<1><<<grid, 256, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+    transform_lm_kernel<1><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, XT, N, g, out);
   else
-    transform_lm_kernel<2><<<grid, 256, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+    transform_lm_kernel<2><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, XT, N, g, out);
   return hipGetLastError();
 }
 
