@@ -141,6 +141,25 @@ def test_fit_resident_kernel_counter_stream(monkeypatch, cfg, n, clauses, epochs
         assert_state_equal(tm, ref, f"epoch {epoch}")
 
 
+def test_stream_kernel_choice_follows_feedback():
+    """One-patch models train on the streaming kernel unless the last fit had feedback at half
+    of its samples or more (then the resident kernel); the counts of samples with feedback
+    agree between the kernels, and every fit matches the oracle."""
+    tm, ref, X, y, *_ = pair(1, 3000)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    kinds = []
+    for epoch in range(3):
+        upd = ref.fit_encoded(encX, encY)
+        tm.fit(encX, y, is_X_encoded=True)
+        st = tm.stats()
+        kinds.append(st["train_kind"])
+        assert st["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+        assert st["last_fit_feedback_samples"] > 1500  # noisy XOR: feedback at nearly every sample
+    assert kinds == [3, 0, 0]
+
+
 @pytest.mark.parametrize("wgs,threads", [("", ""), ("7", ""), ("31", "512"), ("64", "256")])
 def test_fit_stream_launch_shapes(monkeypatch, wgs, threads):
     """The streaming kernel (one patch, counter stream) against the oracle over several
@@ -148,6 +167,7 @@ def test_fit_stream_launch_shapes(monkeypatch, wgs, threads):
     grids (50 clauses per workgroup down to 3) and workgroup sizes."""
     monkeypatch.setenv("YTM_TRAIN_WGS", wgs)
     monkeypatch.setenv("YTM_TRAIN_THREADS", threads)
+    monkeypatch.setenv("YTM_TRAIN_STREAM", "1")  # also where the last fit had feedback at most samples
     tm, ref, X, y, *_ = pair(2, 2000, clauses=200)
     encX = tm.encode(X)
     encY = ref.encode_y_multiclass(y)

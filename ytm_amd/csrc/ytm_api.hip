@@ -45,6 +45,7 @@ struct ytm_model {
   // the state is then a mix of samples: the model refuses fit, score and transform until a
   // whole state is loaded again (the bits of the setters called since: 1 TA states, 2
   // weights, 4 patch weights).
+  double feedback_frac = 0.0;  // share of the last fit's samples where some class could update
   bool invalid = false;
   int reloaded = 0;
   ytm_stats stats;
@@ -520,7 +521,12 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   ytm::TrainKind kind;
   int rng_slots = 0;
   size_t lds = 0;
-  if (stream_geometry(m, inj, global, count, &g)) {
+  // The streaming kernel pays when few samples need feedback: it is taken unless the last
+  // fit had feedback at half of its samples or more (config 1: at nearly every sample, where
+  // the resident kernel is 11% faster), or YTM_TRAIN_STREAM forces it (1) or rules it out (0).
+  const char* stream_env = std::getenv("YTM_TRAIN_STREAM");
+  const bool stream_forced = stream_env && std::atoi(stream_env) > 0;
+  if ((stream_forced || m->feedback_frac < 0.5) && stream_geometry(m, inj, global, count, &g)) {
     kind = ytm::TrainKind::kStream;
     cpw = ytm::kStreamClauses;
     lds = ytm::stream_lds_bytes(g, g.threads);
@@ -656,7 +662,8 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   for (int j = 0; j < 8; ++j) m->stats.last_fit_phase_us[j] = (double)cnt[4 + j] / 100.0 / (double)grid / (double)count;
   const unsigned long long upd = cnt[0];
   m->stats.last_fit_stream = kind == ytm::TrainKind::kStream;
-  m->stats.last_fit_feedback_samples = kind == ytm::TrainKind::kStream ? cnt[12] : (uint64_t)count;
+  m->stats.last_fit_feedback_samples = cnt[12];
+  m->feedback_frac = (double)cnt[12] / (double)count;
   m->stats.last_fit_evaluations = kind == ytm::TrainKind::kStream ? cnt[13] / (uint64_t)grid : (uint64_t)count;
   const bool counted = prof_level() == 4;
   m->stats.last_fit_draws[0] = counted ? cnt[14] : 0;

@@ -1207,7 +1207,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   // several patches: the reservoir thresholds 1.0f / r, r = 0..P (a.inv_rank)
   float* s_invr = (float*)(s_drop + cpw);
   const bool lm = !VANILLA && literal_major(g);
-  unsigned long long my_updates = 0ull;
+  unsigned long long my_updates = 0ull, my_fb = 0ull;  // my_fb: samples where some class may update
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
   const bool prof = a.profile && wave == 0;
@@ -1281,6 +1281,8 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       if (exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part[b], &S, &s_abort, &wait_ticks) &&
           lane < g.K)
         class_targets(g, lane, S + (long long)a.bias[lane], a.Y + (int64_t)i * g.K, s_tgt, s_prob);
+      // samples where some class may update (workgroup 0 counts them)
+      if (wg == 0 && __ballot(lane < g.K && s_prob[lane < g.K ? lane : 0] > 0.0) != 0ull) ++my_fb;
       YTM_PROF_MARK(1);
     } else if (more) {
       global_phase_a<VANILLA, INJECT>(a, g, i + 1, c_begin, n_own, &s_next_a, s_lits, s_nlit, cap, xt_of(i + 1),
@@ -1428,6 +1430,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   for (int64_t j = threadIdx.x; j < n_own * g.K; j += blockDim.x) a.weights[c_begin * g.K + j] = s_wg[j];
   if (lane == 0 && my_updates) atomicAdd(&a.counters[0], my_updates);
   if (threadIdx.x == 0) {
+    if (my_fb) atomicAdd(&a.counters[12], my_fb);
     atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
     atomicAdd(&a.counters[2], (unsigned long long)(__builtin_amdgcn_s_memrealtime() - t_kernel));
     if (prof)
@@ -1783,7 +1786,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   int* s_slot_k = s_slot_idx + R;                                 // [R] class of a draw slot
   uint32_t* s_rng = (uint32_t*)(s_slot_k + R);                    // [R][W][kPreGroups][4]
   float* s_invr = (float*)(s_rng + (int64_t)R * g.W * kPreGroups * 4);  // [P+1] reservoir thresholds 1.0f / r
-  unsigned long long my_updates = 0ull;
+  unsigned long long my_updates = 0ull, my_fb = 0ull;  // my_fb: samples where some class may update
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
   // Optional phase timing (wave 0's view, 100 MHz real-time counter).
@@ -1913,6 +1916,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         YTM_PROF_MARK(0);
         if (ok) {
           const ClassTest fb = class_test(g, S + bias_kk, cp);  // every lane: class kk
+          // samples where some class may update (workgroup 0 counts them)
+          if (wg == 0 && __ballot(fb.num > 0.0) != 0ull) ++my_fb;
 #pragma unroll
           for (int p = 0; p < kFusedPasses; ++p) {
             if (p * cpp >= n_own) continue;  // (no break: the loop must unroll for pre[] to stay in registers)
@@ -1960,6 +1965,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         if (exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part[b2], &S, &s_abort, &wait_ticks) &&
             lane < g.K)
           class_targets(g, lane, S + (long long)s_bias[lane], s_y + b3 * g.K, s_tgt, s_prob);
+        // samples where some class may update (workgroup 0 counts them)
+        if (wg == 0 && __ballot(lane < g.K && s_prob[lane < g.K ? lane : 0] > 0.0) != 0ull) ++my_fb;
         YTM_PROF_MARK(0);
       }
     } else {
@@ -2190,6 +2197,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   if (a.profile && lane == 0 && wave > 0) atomicMax(&s_spec_max, (unsigned long long)spec_ticks);
   __syncthreads();
   if (threadIdx.x == 0) {
+    if (my_fb) atomicAdd(&a.counters[12], my_fb);
     atomicAdd(&a.counters[1], (unsigned long long)wait_ticks);
     atomicAdd(&a.counters[2], (unsigned long long)(__builtin_amdgcn_s_memrealtime() - t_kernel));
     if (prof) {

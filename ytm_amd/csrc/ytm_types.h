@@ -92,7 +92,8 @@ struct TrainArgs {
   const float* inv_rank;     // [P + 1], inv_rank[r] = 1.0f / r
   unsigned long long* slots; // [N][slot_stride], zero on entry
   unsigned long long* counters;  // [0] updated clauses, [1] wait ticks, [2] kernel ticks, [4..11] phases,
-                                 // [12] feedback samples, [13] evaluations (streaming kernel); with
+                                 // [12] samples where some class may update (workgroup 0 counts; the
+                                 // streaming kernel's stops), [13] evaluations (streaming kernel); with
                                  // profile 4, lane draws: [3] Q-skip/update, [14] reservoir, [15] literal
   int* err;                  // {1, sample, workgroup, count} when a bounded wait expires
   int64_t inject_block;
