@@ -1180,6 +1180,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   __shared__ int s_next_a, s_next_d;  // clause claims of phase A and of the decisions
   __shared__ int s_abort;
   __shared__ int s_ntask;
+  __shared__ int s_anyfb;  // some class of the current sample may update
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int nwv = (int)(blockDim.x / kWave);
@@ -1281,8 +1282,12 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       if (exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part[b], &S, &s_abort, &wait_ticks) &&
           lane < g.K)
         class_targets(g, lane, S + (long long)a.bias[lane], a.Y + (int64_t)i * g.K, s_tgt, s_prob);
-      // samples where some class may update (workgroup 0 counts them)
-      if (wg == 0 && __ballot(lane < g.K && s_prob[lane < g.K ? lane : 0] > 0.0) != 0ull) ++my_fb;
+      // samples where some class may update (workgroup 0 counts them); without one, the
+      // sample's feedback (decisions, updates, re-evaluations) is skipped: every update needs
+      // its draw u in (0, 1] at or below a probability above zero (kernel.cu:573-575)
+      const bool anyfb = __ballot(lane < g.K && s_prob[lane < g.K ? lane : 0] > 0.0) != 0ull;
+      if (wg == 0 && anyfb) ++my_fb;
+      if (lane == 0) s_anyfb = anyfb;
       YTM_PROF_MARK(1);
     } else if (more) {
       global_phase_a<VANILLA, INJECT>(a, g, i + 1, c_begin, n_own, &s_next_a, s_lits, s_nlit, cap, xt_of(i + 1),
@@ -1295,6 +1300,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     }
     YTM_PROF_MARK(2);
     if (s_abort) break;
+    if (!s_anyfb) continue;
 
     // ---- 3: decisions of sample i
     for (;;) {
@@ -1751,6 +1757,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   __shared__ double s_prob[64];
   __shared__ int s_abort;
   __shared__ int s_ntask[2], s_nslot[2];  // queued tasks / draw slots, by sample parity
+  __shared__ int s_anyfb;                  // some class of sample i may update (decisions after the exchange)
   __shared__ unsigned long long s_spec_max;  // profile: slowest wave's time in step 1 (waves >= 1)
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
@@ -1965,8 +1972,12 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
         if (exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part[b2], &S, &s_abort, &wait_ticks) &&
             lane < g.K)
           class_targets(g, lane, S + (long long)s_bias[lane], s_y + b3 * g.K, s_tgt, s_prob);
-        // samples where some class may update (workgroup 0 counts them)
-        if (wg == 0 && __ballot(lane < g.K && s_prob[lane < g.K ? lane : 0] > 0.0) != 0ull) ++my_fb;
+        // samples where some class may update (workgroup 0 counts them); without one, D1 is
+        // skipped (every update needs its draw u in (0, 1] at or below a probability above
+        // zero, kernel.cu:573-575)
+        const bool anyfb = __ballot(lane < g.K && s_prob[lane < g.K ? lane : 0] > 0.0) != 0ull;
+        if (wg == 0 && anyfb) ++my_fb;
+        if (lane == 0) s_anyfb = anyfb;
         YTM_PROF_MARK(0);
       }
     } else {
@@ -2028,6 +2039,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
     // (clause, class) pairs, kn classes per clause and 64 / kn clauses per wave pass
     // (decide_pair), and a clause is queued by its first lane.
     if (!fused) {
+      if (!s_anyfb) continue;  // no class of sample i can update: nothing is queued
       if (n_own <= nwv) {
         for (int idx = wave; idx < n_own; idx += nwv) {
           const int64_t c = c_begin + idx;
