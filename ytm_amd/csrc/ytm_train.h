@@ -1289,10 +1289,11 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
       if (wg == 0 && anyfb) ++my_fb;
       if (lane == 0) s_anyfb = anyfb;
       YTM_PROF_MARK(1);
-    } else if (more) {
+    }
+    // phase A of sample i+1: the other waves from the start, wave 0 once it has the totals
+    if (more)
       global_phase_a<VANILLA, INJECT>(a, g, i + 1, c_begin, n_own, &s_next_a, s_lits, s_nlit, cap, xt_of(i + 1),
                                       xe_of(i + 1), s_mask, sel_n, ninc_n, s_wg, s_part[bn], s_invr, s_drop);
-    }
     __syncthreads();
     if (i < 0) {
       prof_last = __builtin_amdgcn_s_memrealtime();
