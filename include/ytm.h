@@ -77,14 +77,16 @@ typedef struct ytm_stats {
     uint64_t total_updates;
     double last_fit_kernel_ms;   /* sum over the training kernel launches of the last fit */
     int32_t last_fit_launches;
-    int32_t train_workgroups;    /* persistent grid size used by the training kernel */
+    int32_t train_workgroups;    /* persistent grid size used by the training kernel (clause
+                                    banks: workgroups of each per-sample launch) */
     double last_score_kernel_ms; /* class-sum kernel of the last score */
     double last_encode_kernel_ms;
     double last_fit_wait_frac;   /* share of the training kernel's time workgroups spent
                                     waiting for the per-sample class sums */
     int32_t train_kind;          /* 0 = clause state resident in LDS, 1 = global (one
                                     patch), 2 = global (several patches), 3 = resident and
-                                    streaming (one patch) */
+                                    streaming (one patch), 4 = clause banks (coalesced=0):
+                                    two ordinary launches per sample */
     int32_t train_specialised;   /* 1 when the last fit ran a training kernel compiled at run
                                     time for this model's geometry (hipRTC), 0 when it ran the
                                     built-in kernel (YTM_JIT=0, or the compile was unavailable) */
@@ -130,6 +132,7 @@ int ytm_set_seed(ytm_model *m, uint64_t seed);
  * MI355X), without touching a GPU.  train_kind as in ytm_stats (0 resident: one patch, or
  * several with ceil(P/32) <= 64; 1 global one patch; 2 global several patches; 3 streaming:
  * one patch, coalesced, counter stream only); injected != 0 for the injected-draw variant.
+ * Clause-bank models (coalesced = 0) train with built-in kernels only: YTM_EINVAL.
  * The counterpart of the per-model kernel compile in BaseTM.__init__
  * (src/cutm/base.py:129-159); ytm_fit compiles on first use anyway, so calling this is
  * optional (warm-up, or checking that the compiler is available).  YTM_EHIP with the

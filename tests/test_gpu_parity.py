@@ -22,10 +22,6 @@ from ytm_amd._lib import YtmError  # noqa: E402
 
 orc.set_threads(min(16, os.cpu_count() or 1))
 
-BANKS_OFF = ("coalesced=False is switched off: its first GPU training run stalled and the cause is not "
-             "yet shown")
-
-
 @pytest.fixture(autouse=True)
 def _specialised_kernels_required(monkeypatch):
     """Training runs the kernels compiled per model (hipRTC); a failed compile is an error
@@ -244,8 +240,7 @@ def test_update_test_at_its_boundaries(T):
 
 @pytest.mark.parametrize(
     "opts",
-    [pytest.param(dict(coalesced=False), marks=pytest.mark.skip(reason=BANKS_OFF)),
-     dict(negative_polarity=False, init_neg_weights=False), dict(max_included_literals=4),
+    [dict(coalesced=False), dict(negative_polarity=False, init_neg_weights=False), dict(max_included_literals=4),
      dict(append_negated=False), dict(number_of_ta_states=16), dict(q=3), dict(q=0.5)],
 )
 def test_fit_variant_flags(opts):
@@ -294,6 +289,46 @@ def test_fit_conv_variant_no_loc():
     tm.fit(encX, y, is_X_encoded=True)
     ref.fit_encoded(encX, ref.encode_y_multiclass(y))
     assert_state_equal(tm, ref)
+
+
+@pytest.mark.parametrize("cfg,n,clauses,opts", [
+    (2, 150, 30, dict()),                                          # one patch
+    (3, 30, 20, dict()),                                           # several patches
+    (5, 60, 40, dict(negative_polarity=False, init_neg_weights=False)),
+    (1, 400, None, dict(max_included_literals=3, q=2)),
+])
+def test_fit_clause_banks(cfg, n, clauses, opts):
+    """Clause banks (coalesced=False, kernel.cu:59-67,306-312,563-565): each clause votes for
+    and learns only its bank's class.  Counter stream, injected draws and a clause drop mask,
+    then scores and clause outputs of the trained model, against the oracle."""
+    tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses, coalesced=False, **opts)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    tm.fit(encX, y, is_X_encoded=True)
+    upd = ref.fit_encoded(encX, encY)
+    assert tm.stats()["train_kind"] == 4
+    assert tm.stats()["last_fit_updates"] == upd
+    assert_state_equal(tm, ref, "counter stream")
+    rng = np.random.default_rng(cfg + 100)
+    inj = rng.random(tm.random_stream_size(n)).astype(np.float32)
+    inj[::13] = 1.0
+    tm.fit(encX, y, is_X_encoded=True, random_stream=inj)
+    upd = ref.fit_encoded(encX, encY, inject=inj)
+    assert tm.stats()["last_fit_updates"] == upd
+    assert_state_equal(tm, ref, "injected")
+    drop_rng = np.random.default_rng(workloads.MODEL_SEED)  # the model's numpy rng (base.py:123,289)
+    tm.fit(encX, y, is_X_encoded=True, clause_drop_p=0.25)
+    drop = (drop_rng.random(ref.C) <= 0.25).astype(np.uint32)
+    upd = ref.fit_encoded(encX, encY, drop=drop)
+    assert tm.stats()["last_fit_updates"] == upd
+    assert_state_equal(tm, ref, "clause drop")
+    w = tm.get_weights().reshape(ref.w.shape)
+    bank = np.arange(ref.C) // (ref.C // w.shape[1])
+    off_bank = np.ones_like(w, dtype=bool)
+    off_bank[np.arange(ref.C), bank] = False
+    assert np.all(w[off_bank] == 0)  # weights outside the own bank stay 0
+    np.testing.assert_array_equal(tm.score(encX, is_X_encoded=True), ref.score(encX))
+    np.testing.assert_array_equal(tm.transform(encX, is_X_encoded=True), ref.transform(encX))
 
 
 def test_clause_drop():
@@ -532,7 +567,6 @@ def _big_view(tm):
     return np.broadcast_to(base, (n,) + base.shape[1:])
 
 
-@pytest.mark.skip(reason=BANKS_OFF)
 def test_non_coalesced_shapes():
     X, y, *_ , kw = workloads.make(2, 50, 1)
     kw.update(number_of_clauses_per_class=6, coalesced=False, seed=3)

@@ -92,9 +92,6 @@ int resolve_geometry(const ytm_params& p, Geom* out) {
   if (p.number_of_ta_states < 1) return fail(YTM_EINVAL, "number_of_ta_states must be >= 1");
   if (!p.coalesced && p.clauses % p.classes != 0)
     return fail(YTM_EINVAL, "non-coalesced clause banks need clauses divisible by classes");
-  // Switched off: its first GPU training run stalled without a cause shown yet.
-  if (!p.coalesced)
-    return fail(YTM_EINVAL, "coalesced=False (clause banks) is disabled in this build");
   g.C = p.clauses;
   g.K = p.classes;
   g.dim0 = p.dim0; g.dim1 = p.dim1; g.dim2 = p.dim2;
@@ -311,6 +308,110 @@ ytm::TrainKind choose_train_kind(Geom* g, int cpw, bool force_global) {
   return kind;
 }
 
+// fit() of a clause-bank model (coalesced=False): two ordinary launches per sample
+// (launch_bank_sample), no persistent kernel and no wait between workgroups.  Slot memory:
+// the class sums of two consecutive samples [2][64] int64, then sel [C] and ninc [C].
+int fit_banks(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count, const uint32_t* drop,
+              const float* inject) {
+  const Geom& g = m->g;
+  const bool inj = inject != nullptr;
+  const int64_t block = g.C * g.P + 2 * g.C * g.K + g.C * g.K * g.L;
+  int64_t chunk = count;  // samples per copy of the injected blocks (<= 1 GiB)
+  if (inj) chunk = std::min<int64_t>(chunk, std::max<int64_t>(1, ((int64_t)1 << 30) / (block * 4)));
+  int rc = ensure_slots(m, (size_t)(2 * 64 * 8 + g.C * 8));
+  if (rc) return rc;
+  long long* sums = (long long*)m->d_slots;
+  int* d_sel = (int*)(sums + 2 * 64);
+  int* d_ninc = d_sel + g.C;
+  uint32_t* d_drop = nullptr;
+  float* d_inj = nullptr;
+  std::vector<uint32_t> zeros;
+  if (!drop) {
+    zeros.assign((size_t)g.C, 0u);
+    drop = zeros.data();
+  }
+  rc = upload((void**)&d_drop, drop, (size_t)g.C * 4, m->stream);
+  if (rc) return rc;
+  if (inj) {
+    hipError_t e = hipMalloc(&d_inj, (size_t)(chunk * block) * 4);
+    if (e != hipSuccess) {
+      (void)hipFree(d_drop);
+      return fail(YTM_EHIP, std::string("hipMalloc(inject) failed: ") + hipGetErrorString(e));
+    }
+  }
+  auto finish = [&](int code) {
+    (void)hipStreamSynchronize(m->stream);
+    (void)hipFree(d_drop);
+    if (d_inj) (void)hipFree(d_inj);
+    return code;
+  };
+#define BANK_TRY(expr)                                                                          \
+  do {                                                                                          \
+    hipError_t e_ = (expr);                                                                     \
+    if (e_ != hipSuccess)                                                                       \
+      return finish(fail(YTM_EHIP, std::string(#expr) + " failed: " + hipGetErrorString(e_)));  \
+  } while (0)
+  BANK_TRY(hipMemsetAsync(m->d_counters, 0, 128, m->stream));
+  BANK_TRY(ytm::launch_fill_u64((unsigned long long*)sums, 2 * 64, m->stream));
+  m->w_bound += (double)count;
+  double ms_total = 0.0;
+  int launches = 0;
+  for (int64_t s = 0; s < count; s += chunk) {
+    const int64_t n = std::min(chunk, count - s);
+    if (inj)
+      BANK_TRY(hipMemcpyAsync(d_inj, inject + s * block, (size_t)(n * block) * 4, hipMemcpyHostToDevice, m->stream));
+    ytm::TrainArgs a{};
+    a.planes = m->d_planes;
+    a.weights = m->d_w;
+    a.patch_w = m->d_pw;
+    a.bias = m->d_bias;
+    a.X = ds->d_X + (first + s) * g.P * g.W;
+    a.Y = ds->d_Y + (first + s) * g.K;
+    a.drop = d_drop;
+    a.inject = d_inj;
+    a.inv_rank = m->d_inv_rank;
+    a.counters = m->d_counters;
+    a.err = m->d_err;
+    a.inject_block = block;
+    a.step0 = m->stats.step + (uint64_t)s;
+    a.seed = m->params.seed;
+    a.N = (int)n;
+    a.g = g;
+    BANK_TRY(hipEventRecord(m->ev0, m->stream));
+    for (int64_t i = 0; i < n; ++i) {
+      const int row = (int)((s + i) & 1);
+      BANK_TRY(ytm::launch_bank_sample(a, (int)i, sums + row * 64, sums + (row ^ 1) * 64, d_sel, d_ninc, inj,
+                                       m->stream));
+    }
+    BANK_TRY(hipEventRecord(m->ev1, m->stream));
+    BANK_TRY(hipEventSynchronize(m->ev1));
+    float ms = 0.0f;
+    BANK_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+    ms_total += ms;
+    launches += (int)(2 * n);
+  }
+  unsigned long long cnt[16] = {0};
+  BANK_TRY(hipMemcpy(cnt, m->d_counters, sizeof(cnt), hipMemcpyDeviceToHost));
+#undef BANK_TRY
+  for (int j = 0; j < 8; ++j) m->stats.last_fit_phase_us[j] = 0.0;
+  m->stats.last_fit_stream = 0;
+  m->stats.last_fit_feedback_samples = cnt[12];
+  m->feedback_frac = (double)cnt[12] / (double)count;
+  m->stats.last_fit_evaluations = (uint64_t)count;
+  for (int j = 0; j < 3; ++j) m->stats.last_fit_draws[j] = 0;
+  m->stats.last_fit_wait_frac = 0.0;
+  m->stats.train_kind = (int32_t)ytm::TrainKind::kBanks;
+  m->stats.train_specialised = 0;
+  m->stats.train_workgroups = (int32_t)std::min<int64_t>((g.C * 64 + 255) / 256, 65536);  // per launch
+  m->stats.step += (uint64_t)count;
+  m->stats.last_fit_samples = (uint64_t)count;
+  m->stats.last_fit_updates = cnt[0];
+  m->stats.total_updates += cnt[0];
+  m->stats.last_fit_kernel_ms = ms_total;
+  m->stats.last_fit_launches = launches;
+  return finish(YTM_OK);
+}
+
 }  // namespace
 
 extern "C" {
@@ -386,6 +487,8 @@ int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injec
   Geom model;
   int rc = resolve_geometry(*params, &model);
   if (rc) return rc;
+  if (!model.coalesced)
+    return fail(YTM_EINVAL, "clause banks (coalesced=False) train with built-in kernels; none is compiled per model");
   if (train_kind == 3) {
     Geom gs;
     if (injected || !stream_shape(model, compute_units > 0 ? compute_units : 256, &gs))
@@ -513,6 +616,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   m->stats.last_fit_kernel_ms = 0.0;
   m->stats.last_fit_launches = 0;
   if (count == 0) return YTM_OK;
+  if (!m->g.coalesced) return fit_banks(m, ds, first, count, drop, inject);
   const bool inj = inject != nullptr;
   const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
   const bool global = force_global && std::atoi(force_global) > 0;
