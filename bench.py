@@ -205,7 +205,7 @@ def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=No
         elif os.environ.get("YTM_TRAIN_PROFILE"):
             names = {0: ("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier", "step1-slowest-wave"),
                      3: ("stream", "drain", "decide", "apply")}.get(
-                         ep["kind"], ("publish+stage", "exchange", "next-A-wait", "decide", "apply", "re-eval"))
+                         ep["kind"], ("stage", "publish+exchange", "next-A-wait", "decide", "apply", "re-eval"))
             log("[bench]   phase us/sample (wave 0): " + " ".join(f"{n} {v:.2f}" for n, v in zip(names, ep["phase"])))
             if ep["kind"] == 3 and ep["feedback"]:
                 log("[bench]   per stop, us: " + " ".join(f"{n} {v * N / ep['feedback']:.2f}"

@@ -94,7 +94,7 @@ typedef struct ytm_stats {
                                     that wave 0 of each workgroup spends in each phase of the
                                     training kernel (resident: exchange, barrier, D1, barrier,
                                     D2, D3, barrier, and the slowest other wave's time in the
-                                    exchange step; global: publish and staging, exchange,
+                                    exchange step; global: staging, publish and exchange,
                                     wait for the next sample's evaluation, decisions, literal
                                     updates, re-evaluation of the updated clauses).  YTM_TRAIN_PROFILE=2 / =3 restrict that last
                                     resident slot to the next sample's evaluation / its

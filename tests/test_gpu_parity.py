@@ -291,6 +291,33 @@ def test_fit_conv_variant_no_loc():
     assert_state_equal(tm, ref)
 
 
+@pytest.mark.parametrize("halves_env", ["", "0"])
+def test_encoded_samples_without_complement_halves(monkeypatch, halves_env):
+    """Samples encoded elsewhere (fit(is_X_encoded=True)) need not hold the negated literals as
+    the complements of the others.  Where they do, the several-patch training kernels stage
+    only the first half of a sample's literal-major copy and complement it; where they do
+    not (bits flipped here), the whole copy.  Both against the oracle; YTM_TRAIN_XT_HALVES=0
+    stages the whole copy either way."""
+    monkeypatch.setenv("YTM_TRAIN_GLOBAL", "1")
+    monkeypatch.setenv("YTM_TRAIN_XT_HALVES", halves_env)
+    tm, ref, X, y, *_ = pair(4, 8, clauses=40)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    L = tm.number_of_literals
+    rng = np.random.default_rng(3)
+    odd = encX.copy()
+    for e in range(0, len(odd), 2):  # every other sample: a few literals of a few patches flipped
+        for _ in range(5):
+            p, l = rng.integers(tm.number_of_patches), rng.integers(L)
+            odd[e, p, l // 32] ^= np.uint32(1 << (l % 32))
+    for data in (encX, odd):
+        tm.fit(data, y, is_X_encoded=True)
+        upd = ref.fit_encoded(data, encY)
+        assert tm.stats()["train_kind"] == 2
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref)
+
+
 @pytest.mark.parametrize("cfg,n,clauses,opts", [
     (2, 150, 30, dict()),                                          # one patch
     (3, 30, 20, dict()),                                           # several patches

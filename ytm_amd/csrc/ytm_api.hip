@@ -57,6 +57,7 @@ struct ytm_dataset {
   int32_t* d_Y;    // [N][K]
   int64_t N;
   uint32_t* d_XT;  // [N][L][ceil(P/32)] literal-major copy (several patches), or null
+  int xt_halves;   // d_XT's literals Lh..L-1 are the complements of 0..Lh-1 (TrainArgs::xt_halves)
 };
 
 namespace {
@@ -575,7 +576,7 @@ int ytm_dataset_create(ytm_model* m, const uint32_t* encX, const int32_t* encY, 
   if (!m || !out || N < 0 || (N > 0 && !encX)) return fail(YTM_EINVAL, "bad dataset arguments");
   *out = nullptr;
   const Geom& g = m->g;
-  ytm_dataset* ds = new ytm_dataset{m, nullptr, nullptr, N, nullptr};
+  ytm_dataset* ds = new ytm_dataset{m, nullptr, nullptr, N, nullptr, 0};
   int rc = upload((void**)&ds->d_X, encX, (size_t)(N * g.P * g.W) * 4, m->stream);
   if (!rc && encY) rc = upload((void**)&ds->d_Y, encY, (size_t)(N * g.K) * 4, m->stream);
   if (!rc && ytm::literal_major(g) && N > 0) {
@@ -583,6 +584,19 @@ int ytm_dataset_create(ytm_model* m, const uint32_t* encX, const int32_t* encY, 
     const size_t bytes = (size_t)(N * g.L * ((g.P + 31) / 32)) * 4;
     hipError_t e = hipMalloc(&ds->d_XT, bytes);
     if (e == hipSuccess) e = ytm::launch_transpose(ds->d_X, N, ds->d_XT, g, m->stream);
+    if (e == hipSuccess && g.append_negated) {
+      // Encoded samples hold the negations as complements (BaseTM.encode); samples encoded
+      // elsewhere may not, so the training kernels rely on it only where this check holds.
+      int* d_ok = nullptr;
+      int ok = 1;
+      e = hipMalloc(&d_ok, sizeof(int));
+      if (e == hipSuccess) e = hipMemcpyAsync(d_ok, &ok, sizeof(int), hipMemcpyHostToDevice, m->stream);
+      if (e == hipSuccess) e = ytm::launch_xt_halves_check(ds->d_XT, N, g, d_ok, m->stream);
+      if (e == hipSuccess) e = hipMemcpyAsync(&ok, d_ok, sizeof(int), hipMemcpyDeviceToHost, m->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+      if (d_ok) (void)hipFree(d_ok);
+      ds->xt_halves = e == hipSuccess && ok == 1;
+    }
     if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("literal-major copy: ") + hipGetErrorString(e));
   }
   if (!rc) {
@@ -735,6 +749,8 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.cpw = cpw;
     a.rng_slots = rng_slots;
     a.profile = prof_level();
+    const char* xh_env = std::getenv("YTM_TRAIN_XT_HALVES");  // 0: stage the whole literal-major copy
+    a.xt_halves = ds->xt_halves && !(xh_env && std::atoi(xh_env) == 0);
     const char* tt_env = std::getenv("YTM_TRAIN_TEST_TIMEOUT");  // test hook of the timeout path
     a.test_timeout = tt_env && std::atoi(tt_env) > 0;
     a.g = g;

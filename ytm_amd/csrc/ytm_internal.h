@@ -14,6 +14,8 @@ namespace ytm {
 hipError_t launch_encode(const uint32_t* X, int64_t N, uint32_t* out, const Geom& g, hipStream_t s);
 // Literal-major copy of encoded samples (several patches): XT [N][L][ceil(P/32)].
 hipError_t launch_transpose(const uint32_t* X, int64_t N, uint32_t* XT, const Geom& g, hipStream_t s);
+// Clears *ok unless every literal Lh + f of XT is the complement of literal f (ok set before).
+hipError_t launch_xt_halves_check(const uint32_t* XT, int64_t N, const Geom& g, int* ok, hipStream_t s);
 hipError_t launch_ta_to_planes(const uint32_t* ta, uint32_t* planes, const Geom& g, hipStream_t s);
 hipError_t launch_planes_to_ta(const uint32_t* planes, uint32_t* ta, const Geom& g, hipStream_t s);
 hipError_t launch_init_state(uint32_t* planes, float* w, const Geom& g, uint64_t seed, hipStream_t s);

@@ -100,6 +100,23 @@ __global__ __launch_bounds__(256) void transpose_kernel(const uint32_t* __restri
   }
 }
 
+// Clears *ok when some literal Lh + f of XT is not the complement of literal f in every
+// patch (bits of patches >= P: 0 in both), i.e. when the training kernels may not stage
+// only the first half of each sample's copy (TrainArgs::xt_halves).  *ok is set before.
+__global__ __launch_bounds__(256) void xt_halves_kernel(const uint32_t* __restrict__ XT, int64_t N, Geom g,
+                                                        int* ok) {
+  const int64_t PW = (g.P + 31) / 32;
+  const int64_t nh = g.Lh * PW;
+  const uint32_t lastm = (g.P & 31) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu;
+  const int64_t n = N * nh;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e = idx / nh, j = idx % nh;
+    const uint32_t* row = XT + e * g.L * PW;
+    if (row[nh + j] != (~row[j] & (j % PW == PW - 1 ? lastm : 0xFFFFFFFFu))) *ok = 0;
+  }
+}
+
 // ===================================================================== TA state I/O
 // uint32 (C, L) states <-> bit-planes.  Literals >= L of the last word hold s = 0 and are
 // never updated or included.
@@ -800,6 +817,11 @@ hipError_t launch_encode(const uint32_t* X, int64_t N, uint32_t* out, const Geom
 hipError_t launch_transpose(const uint32_t* X, int64_t N, uint32_t* XT, const Geom& g, hipStream_t s) {
   const int64_t waves = N * g.W * ((g.P + kWave - 1) / kWave);
   transpose_kernel<<<grid_for(waves * kWave, 256), 256, 0, s>>>(X, N, g, XT);
+  return hipGetLastError();
+}
+
+hipError_t launch_xt_halves_check(const uint32_t* XT, int64_t N, const Geom& g, int* ok, hipStream_t s) {
+  xt_halves_kernel<<<grid_for(N * g.Lh * ((g.P + 31) / 32), 256), 256, 0, s>>>(XT, N, g, ok);
   return hipGetLastError();
 }
 

@@ -1055,6 +1055,33 @@ __device__ __forceinline__ void copy_to_lds(uint32_t* dst, const uint32_t* src, 
   }
 }
 
+// The literal-major copy of a sample whose literals Lh..L-1 are the complements of literals
+// 0..Lh-1 (appended negations; TrainArgs::xt_halves): only the first half, nh = Lh * PW
+// words, is read, and the second half is written as its complement with the bits of
+// patches >= P (in each row's last word) kept 0, as the transposition leaves them.
+__device__ __forceinline__ void copy_halves_to_lds(const Geom& g, uint32_t* dst, const uint32_t* src, int first,
+                                                   int count) {
+  const int64_t PW = (g.P + 31) / 32;
+  const int64_t nh = g.Lh * PW;
+  const uint32_t lastm = (g.P & 31) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu;
+  for (int64_t j0 = first; j0 < nh; j0 += (int64_t)count * kCopyBatch) {
+    uint32_t v[kCopyBatch];
+#pragma unroll
+    for (int b = 0; b < kCopyBatch; ++b) {  // unconditional (clamped) loads, all in flight together
+      const int64_t j = j0 + (int64_t)b * count;
+      v[b] = src[j < nh ? j : nh - 1];
+    }
+#pragma unroll
+    for (int b = 0; b < kCopyBatch; ++b) {
+      const int64_t j = j0 + (int64_t)b * count;
+      if (j < nh) {
+        dst[j] = v[b];
+        dst[nh + j] = ~v[b] & (j % PW == PW - 1 ? lastm : 0xFFFFFFFFu);
+      }
+    }
+  }
+}
+
 // Phase A of the global kernel for several patches with literal lists: waves claim 64 / S
 // clauses at a time from *s_next and evaluate them in lane groups (eval_select_lm_group);
 // clauses without a list take the include-mask walk in global memory, a wave each.  Results
@@ -1238,7 +1265,12 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   // xe_of.
   auto stage = [&](int j, int first, int count) {
     if (g.mask_lds) copy_to_lds(s_xs + (int64_t)(j & 1) * g.W, a.X + (int64_t)j * g.W, g.W, first, count);
-    if (lm && literal_major_lds(g)) copy_to_lds(s_xt, a.XT + (int64_t)j * xt_words, xt_words, first, count);
+    if (lm && literal_major_lds(g)) {
+      if (a.xt_halves)
+        copy_halves_to_lds(g, s_xt, a.XT + (int64_t)j * xt_words, first, count);
+      else
+        copy_to_lds(s_xt, a.XT + (int64_t)j * xt_words, xt_words, first, count);
+    }
   };
   auto xt_of = [&](int j) -> const uint32_t* {
     return !lm ? nullptr : (literal_major_lds(g) ? s_xt : a.XT + (int64_t)j * xt_words);
@@ -1259,13 +1291,8 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     int* sel_n = s_sel + bn * cpw;
     int* ninc_n = s_ninc + bn * cpw;
 
-    // ---- 1: patch weights and publish of sample i; staging of sample i+1
+    // ---- 1: staging of sample i+1
     if (i >= 0 && wave == 0) {
-      for (int idx = lane; idx < n_own; idx += kWave) {
-        const int sl = sel_i[idx];
-        if (sl >= 0) atomicAdd(&a.patch_w[(c_begin + idx) * g.P + sl], 1);
-      }
-      exchange_publish(a, g, i, s_part[b]);
       if (lane == 0) {
         s_next_a = 0;
         s_next_d = 0;
@@ -1276,8 +1303,14 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     __syncthreads();
     YTM_PROF_MARK(0);
 
-    // ---- 2: the totals of sample i (wave 0); speculative phase A of sample i+1 (the others)
+    // ---- 2: the totals of sample i (wave 0, which publishes them first: the other waves
+    // need not wait for that); speculative phase A of sample i+1 (the others)
     if (i >= 0 && wave == 0) {
+      for (int idx = lane; idx < n_own; idx += kWave) {
+        const int sl = sel_i[idx];
+        if (sl >= 0) atomicAdd(&a.patch_w[(c_begin + idx) * g.P + sl], 1);
+      }
+      exchange_publish(a, g, i, s_part[b]);
       long long S = 0;
       if (exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part[b], &S, &s_abort, &wait_ticks) &&
           lane < g.K)

@@ -105,6 +105,7 @@ struct TrainArgs {
   int rng_slots;             // literal-draw slots precomputed per sample (resident kernel)
   int profile;               // accumulate per-phase times into counters[4..11]; 4: count draws instead
   int test_timeout;          // test hook: class-sum waits never see their sums and expire at once
+  int xt_halves;             // XT's literals Lh..L-1 are the complements of 0..Lh-1 (checked per dataset)
   Geom g;
 };
 
