@@ -1272,6 +1272,32 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         copy_to_lds(s_xt, a.XT + (int64_t)j * xt_words, xt_words, first, count);
     }
   };
+  // The same staging from registers, for the words of one-patch samples (mask_lds): each
+  // thread's share of the sample after next is loaded one iteration ahead, so that staging
+  // a sample is an LDS write (config 5: 373 -> 350 ms per epoch).  Not for literal-major
+  // copies: their eight words per thread made config 4's kernel spill (499 -> 596 ms).
+  constexpr int kStagePre = 8;
+  const int64_t stage_n = g.mask_lds ? g.W : 0;
+  const int per = (int)((stage_n + g.threads - 1) / g.threads);
+  const bool prefetched = stage_n > 0 && per <= kStagePre;
+  uint32_t pre[kStagePre];
+  auto prefetch = [&](int j) {
+    const uint32_t* src = a.X + (int64_t)j * g.W;
+#pragma unroll
+    for (int q = 0; q < kStagePre; ++q) {
+      const int64_t idx = threadIdx.x + (int64_t)q * g.threads;
+      if (q < per) pre[q] = src[idx < stage_n ? idx : stage_n - 1];  // clamped: every load unconditional
+    }
+  };
+  auto commit = [&](int j) {
+#pragma unroll
+    for (int q = 0; q < kStagePre; ++q) {
+      const int64_t idx = threadIdx.x + (int64_t)q * g.threads;
+      if (q < per && idx < stage_n) {
+        s_xs[(int64_t)(j & 1) * g.W + idx] = pre[q];
+      }
+    }
+  };
   auto xt_of = [&](int j) -> const uint32_t* {
     return !lm ? nullptr : (literal_major_lds(g) ? s_xt : a.XT + (int64_t)j * xt_words);
   };
@@ -1280,6 +1306,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   };
   const int kn = g.coalesced ? (int)g.K : 1;
   const int cpp = kWave / kn;
+  if (prefetched && a.N > 0) prefetch(0);
   // i = -1 is the prologue: every wave stages sample 0 and takes part in its phase A
   for (int i = -1; i < a.N; ++i) {
     const uint64_t t = a.step0 + (uint64_t)i;
@@ -1299,7 +1326,14 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         s_ntask = 0;
       }
     }
-    if (more) stage(i + 1, threadIdx.x, blockDim.x);
+    if (more) {
+      if (prefetched) {
+        commit(i + 1);
+        if (i + 2 < a.N) prefetch(i + 2);
+      } else {
+        stage(i + 1, threadIdx.x, blockDim.x);
+      }
+    }
     __syncthreads();
     YTM_PROF_MARK(0);
 
