@@ -139,6 +139,13 @@ int ytm_set_seed(ytm_model *m, uint64_t seed);
  * compiler log in ytm_last_error() on failure. */
 int ytm_compile_train_kernel(const ytm_params *params, int train_kind, int injected,
                              int compute_units);
+/* Compile (when not cached) and load onto the model's device every counter-stream training
+ * kernel that ytm_fit may choose for this model (the streaming kernel of a one-patch model and
+ * the resident or global one), so that no fit pays for it later; the kinds loaded (train_kind
+ * values) go to kinds[0 .. *n_kinds).  The counterpart of the per-model kernel compile in
+ * BaseTM.__init__ (src/cutm/base.py:129-159).  Nothing is loaded for clause banks or with
+ * YTM_JIT=0 (*n_kinds = 0).  Optional: ytm_fit loads a kernel on first use anyway. */
+int ytm_load_train_kernels(ytm_model *m, int32_t kinds[4], int32_t *n_kinds);
 
 /* encode: BaseTM.encode (src/cutm/base.py:224-263; kernel.cu:76-152 encode_batch).
  * X: uint32 (N, dim0*dim1*dim2), any value > 0 is a set pixel.  out: uint32 (N, P, W). */

@@ -594,6 +594,26 @@ def _big_view(tm):
     return np.broadcast_to(base, (n,) + base.shape[1:])
 
 
+@pytest.mark.parametrize("cfg,clauses,opts,want", [
+    (2, 300, {}, ([3, 0],)),               # one patch: streaming, then resident
+    (4, 40, {}, ([0], [2])),               # several patches: resident or global, as the LDS allows
+    (2, 30, dict(coalesced=False), ([],)),  # clause banks: built-in kernels only
+])
+def test_load_kernels(cfg, clauses, opts, want):
+    """load_kernels() loads the training kernels a model's fits choose between; fits after it
+    take those kinds and still match the oracle."""
+    tm, ref, X, y, *_ = pair(cfg, 30, clauses=clauses, **opts)
+    kinds = tm.load_kernels()
+    assert kinds in want
+    encX = tm.encode(X)
+    for _ in range(2):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+        assert tm.stats()["last_fit_updates"] == upd
+        assert tm.stats()["train_kind"] in (kinds or [4])
+    assert_state_equal(tm, ref)
+
+
 def test_non_coalesced_shapes():
     X, y, *_ , kw = workloads.make(2, 50, 1)
     kw.update(number_of_clauses_per_class=6, coalesced=False, seed=3)

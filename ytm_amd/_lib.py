@@ -74,6 +74,7 @@ SIGNATURES = {
     "ytm_get_stats": (ctypes.c_int, [_P, ctypes.POINTER(YtmStats)]),
     "ytm_set_seed": (ctypes.c_int, [_P, ctypes.c_uint64]),
     "ytm_compile_train_kernel": (ctypes.c_int, [ctypes.POINTER(YtmParams), ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "ytm_load_train_kernels": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
     "ytm_encode": (ctypes.c_int, [_P, _P, _I64, _P]),
     "ytm_dataset_create": (ctypes.c_int, [_P, _P, _P, _I64, ctypes.POINTER(_P)]),
     "ytm_dataset_destroy": (None, [_P]),

@@ -204,6 +204,15 @@ class BaseTM:
             kinds.append(3)
         return kinds
 
+    def load_kernels(self) -> list[int]:
+        """Compile (when not cached) and load onto this model's GPU every training kernel its
+        fits may switch between, so that no fit pays for the load (about half a second the
+        first time).  Returns the training-kernel kinds loaded (none for clause banks)."""
+        kinds = (ctypes.c_int32 * 4)()
+        n = ctypes.c_int32(0)
+        check(lib.ytm_load_train_kernels(self._handle, kinds, ctypes.byref(n)))
+        return list(kinds[:n.value])
+
     def _gpu_init(self) -> None:
         if getattr(self, "_skip_gpu_init", False):
             self._handle = None

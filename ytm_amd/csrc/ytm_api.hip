@@ -481,6 +481,27 @@ void ytm_destroy(ytm_model* m) {
   delete m;
 }
 
+int ytm_load_train_kernels(ytm_model* m, int32_t kinds[4], int32_t* n_kinds) {
+  if (!m || !kinds || !n_kinds) return fail(YTM_EINVAL, "null argument");
+  *n_kinds = 0;
+  if (!m->g.coalesced || !ytm::jit_enabled()) return YTM_OK;  // built-in kernels only
+  const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
+  const bool global = force_global && std::atoi(force_global) > 0;
+  auto load = [&](const Geom& g, ytm::TrainKind kind) {
+    std::string why;
+    if (!ytm::jit_train_kernel(g, kind, false, &why)) return fail(YTM_EHIP, "training kernel: " + why);
+    kinds[(*n_kinds)++] = (int32_t)kind;
+    return (int)YTM_OK;
+  };
+  Geom gs;
+  if (stream_geometry(m, false, global, 0, &gs))
+    if (int rc = load(gs, ytm::TrainKind::kStream)) return rc;
+  int cpw;
+  Geom g = train_geometry(m->g, m->cus, &cpw);
+  const ytm::TrainKind kind = choose_train_kind(&g, cpw, global);
+  return load(g, kind);
+}
+
 int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injected, int compute_units) {
   if (!params) return fail(YTM_EINVAL, "null params");
   if (train_kind < 0 || train_kind > 3) return fail(YTM_EINVAL, "train_kind must be 0, 1, 2 or 3");
