@@ -156,13 +156,18 @@ def test_stream_kernel_choice_follows_feedback():
     assert kinds == [3, 0, 0]
 
 
-@pytest.mark.parametrize("wgs,threads", [("", ""), ("7", ""), ("31", "512"), ("64", "256")])
-def test_fit_stream_launch_shapes(monkeypatch, wgs, threads):
+@pytest.mark.parametrize("wgs,threads,gens", [("", "", ""), ("7", "", ""), ("31", "512", ""), ("64", "256", ""),
+                                              ("", "", "1"), ("7", "", "3")])
+def test_fit_stream_launch_shapes(monkeypatch, wgs, threads, gens):
     """The streaming kernel (one patch, counter stream) against the oracle over several
     epochs, as training moves from feedback on most samples to feedback on few, for several
-    grids (50 clauses per workgroup down to 3) and workgroup sizes."""
+    grids (50 clauses per workgroup down to 3) and workgroup sizes.  A stream normally goes
+    on past each stop (the rows published past it get the updated clauses' vote
+    differences); YTM_TRAIN_STREAM_GENS makes it start a fresh one on fresh rows every
+    1 or 3 stops instead."""
     monkeypatch.setenv("YTM_TRAIN_WGS", wgs)
     monkeypatch.setenv("YTM_TRAIN_THREADS", threads)
+    monkeypatch.setenv("YTM_TRAIN_STREAM_GENS", gens)
     monkeypatch.setenv("YTM_TRAIN_STREAM", "1")  # also where the last fit had feedback at most samples
     tm, ref, X, y, *_ = pair(2, 2000, clauses=200)
     encX = tm.encode(X)

@@ -770,6 +770,8 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.cpw = cpw;
     a.rng_slots = rng_slots;
     a.profile = prof_level();
+    const char* sg_env = std::getenv("YTM_TRAIN_STREAM_GENS");  // test hook: stops per stream
+    a.stream_gens = sg_env ? std::max(0, std::atoi(sg_env)) : 0;
     const char* xh_env = std::getenv("YTM_TRAIN_XT_HALVES");  // 0: stage the whole literal-major copy
     a.xt_halves = ds->xt_halves && !(xh_env && std::atoi(xh_env) == 0);
     const char* tt_env = std::getenv("YTM_TRAIN_TEST_TIMEOUT");  // test hook of the timeout path

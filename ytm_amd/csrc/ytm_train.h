@@ -2302,15 +2302,19 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
 // weights; the rows already published for later samples stay exact because nothing
 // changed.  The first sample with some prob > 0 stops the stream in every workgroup (all
 // see the same sums): the workgroup takes that sample's feedback decisions and literal
-// updates (the same functions as the resident kernel), and streaming restarts at the next
-// sample on fresh rows, so the speculative rows published past the stop are never read.
+// updates (the same functions as the resident kernel).  The rows it published past the
+// stop were evaluated with the state before the feedback; only its updated clauses vote
+// differently now, so it adds their vote differences to each such row as one more unit,
+// and streaming goes on at the next sample.  After k stops in a stream every row is
+// complete at G * (k + 1) units: a row published from then on carries k + 1 units at once.
 // The result is exactly the sequential one.
 //
 // Rows of a stream that starts at sample b with first row r0: row(s) = r0 + (s - b).  A
 // workgroup publishes a sample only while it is fewer than kStreamDepth samples ahead of
-// the one it consumes, so a stream that stops at sample j used rows below r0 + (j - b) +
-// kStreamDepth; the next stream starts at row r0 + (j + 1 - b) + kStreamDepth.  Every
-// workgroup derives the same rows from the same stops.
+// the one it consumes.  Once a stream has taken as many stops as the unit count allows
+// (or a.stream_gens), the next one starts on fresh rows past the stop sample j: at row
+// r0 + (j + 1 - b) + kStreamDepth, so the rows published past the stop are never read.
+// Every workgroup derives the same rows from the same stops.
 struct StreamCtl {
   int claim;    // next sample to evaluate
   int consume;  // next sample to consume: every earlier sample of this stream is final
@@ -2329,6 +2333,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   extern __shared__ long long dyn_lds[];
   __shared__ StreamCtl ctl;
   __shared__ unsigned long long s_ring[kStreamDepth];  // selected clauses of in-flight samples
+  __shared__ int s_pub[kStreamDepth];                  // the sample of each ring slot this workgroup published
   __shared__ long long s_S[64];                        // class sums + bias of the stop sample
   __shared__ int s_ntask;
   const int lane = lane_id();
@@ -2341,10 +2346,10 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   const int K = (int)g.K;
   const int64_t Wp = (g.W + 3) & ~(int64_t)3;
   constexpr int D = kStreamDepth;
-  // LDS (sizes in train_lds_bytes): task masks [64][3] u64; planes [64][np][W]; weights
+  // LDS (sizes in stream_lds_bytes): task masks [64][3] u64; planes [64][np][W]; weights
   // [64][K]; transposed integer weights [K][64]; include counts, drop, patch weights, task
   // clauses, zeros, selections of the stop sample [64] each; targets ring [D][K];
-  // complemented samples [waves][Wp].
+  // complemented samples ring [D][Wp]; integer weights before a stop [K][64].
   unsigned long long* s_task_m = (unsigned long long*)dyn_lds;
   uint32_t* s_planes = (uint32_t*)(s_task_m + 3 * kStreamClauses);
   float* s_w = (float*)(s_planes + (int64_t)kStreamClauses * cw);
@@ -2357,6 +2362,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   int* s_selj = s_zero + kStreamClauses;
   int32_t* s_yring = s_selj + kStreamClauses;
   uint32_t* s_nx = (uint32_t*)(s_yring + D * K);
+  int* s_wt_old = (int*)(s_nx + (int64_t)D * Wp);  // [K][64] integer weights before a stop
   const bool exact_count = g.maxinc < g.L;
   const int ks = (K + 15) & ~15;
   unsigned long long my_updates = 0ull, my_evals = 0ull, my_stops = 0ull;
@@ -2389,15 +2395,22 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   const bool prof = a.profile && wave == 0;
   uint64_t prof_acc[4] = {0, 0, 0, 0};
   uint64_t prof_last = t_kernel;
-  int gen_start = 0;
+  int gen_start = 0;  // first sample of the stream (row row_base)
   int64_t row_base = 0;
-  // Lookahead at the start of a stream: twice the previous stream's length (2 to D), so that
+  int next = 0;  // first sample of the current phase (after the last stop)
+  int kgen = 0;  // stops in this stream: every row is complete at G * (kgen + 1) units
+  // Stops a stream may take before a fresh one starts (the unit count of a row must stay
+  // below 2^19); a.stream_gens lowers it (test hook).
+  int kgen_cap = (1 << 19) / G - 2;
+  if (a.stream_gens > 0 && a.stream_gens < kgen_cap) kgen_cap = a.stream_gens;
+  // Lookahead at the start of a phase: twice the previous phase's length (2 to D), so that
   // speculation stays shallow while stops are frequent and is deep as soon as they are rare.
   int depth0 = 2;
-  while (gen_start < a.N) {
+  for (int q = threadIdx.x; q < D; q += blockDim.x) s_pub[q] = -1;
+  while (next < a.N) {
     if (threadIdx.x == 0) {
-      ctl.claim = gen_start;
-      ctl.consume = gen_start;
+      ctl.claim = next;
+      ctl.consume = next;
       ctl.stop = -1;
       ctl.abort = 0;
     }
@@ -2407,10 +2420,11 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       const int nq = K <= 32 ? kWave / K : 1;
       const int q = lane / K, k = lane - (lane / K) * K;
       const long long bias_k = (long long)a.bias[k];
-      int j = gen_start;
+      int j = next;
       int stop = -1;
       // a count no word reaches under the test hook: every wait then expires
-      const unsigned long long complete = (unsigned long long)G + (a.test_timeout ? 1ull : 0ull);
+      const unsigned long long units = (unsigned long long)G * (unsigned long long)(kgen + 1);
+      const unsigned long long complete = units + (a.test_timeout ? 1ull : 0ull);
       while (j < a.N) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         bool here = q < nq && j + q < a.N;  // this lane's (row, class) exists
@@ -2448,7 +2462,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // the rows' LDS rings are written
         // feedback possible in row q?  prob > 0 for some class (class_fb, kernel.cu:508-529)
         const bool live = here && q < ncomp;
-        const long long S = (long long)(v - ((unsigned long long)G << 44)) + bias_k;
+        const long long S = (long long)(v - (units << 44)) + bias_k;
         bool fb = false;
         if (live) {
           const int y = s_yring[((j + q) & (D - 1)) * K + k];
@@ -2472,7 +2486,6 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       if (lane == 0) lds_store(&ctl.stop, stop >= 0 ? stop : a.N);
     } else {
       // ---- evaluation: claim samples in order, evaluate with the current state, publish
-      uint32_t* nx = s_nx + (int64_t)(wave - 1) * Wp;
       const bool own = lane < n_own;
       const uint32_t* m = s_planes + (int64_t)(own ? lane : 0) * cw + (int64_t)(g.np - 1) * g.W;
       for (;;) {
@@ -2481,12 +2494,12 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         if (lane == 0) s = atomicAdd(&ctl.claim, 1);
         s = lane_value(s, 0);
         if (s >= a.N) break;
-        // at most min(D, depth0 + consumed samples of this stream) ahead of the consumer
+        // at most min(D, depth0 + consumed samples of this phase) ahead of the consumer
         bool skip = false;
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         for (unsigned spins = 1;; ++spins) {
           const int cons = lds_load(&ctl.consume);
-          const int ahead = depth0 + (cons - gen_start) < D ? depth0 + (cons - gen_start) : D;
+          const int ahead = depth0 + (cons - next) < D ? depth0 + (cons - next) : D;
           if (s < cons + ahead) break;
           if (lds_load(&ctl.stop) >= 0) {  // stopped before s: s is past the stop sample
             skip = true;
@@ -2507,7 +2520,10 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           __builtin_amdgcn_s_sleep(1);
         }
         if (skip) break;
-        // the sample's complemented words (broadcast reads below) and its targets
+        if (s_pub[s & (D - 1)] == s) continue;  // published before the last stop, and repaired
+        // the sample's complemented words (broadcast reads below; kept in the sample's ring
+        // slot for the repairs after a stop) and its targets
+        uint32_t* nx = s_nx + (int64_t)(s & (D - 1)) * Wp;
         for (int64_t w = lane; w < g.W; w += kWave) nx[w] = ~a.X[(int64_t)s * g.W + w];
         if (lane < K) s_yring[(s & (D - 1)) * K + lane] = a.Y[(int64_t)s * K + lane];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -2532,12 +2548,15 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
             const int p = wave_sum_i32(sel ? s_wt[kk * kStreamClauses + lane] : 0);
             if (lane == kk) mine = p;
           }
-        if (lane == 0) s_ring[s & (D - 1)] = smask;
+        if (lane == 0) {
+          s_ring[s & (D - 1)] = smask;
+          s_pub[s & (D - 1)] = s;
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // ring and targets before the publish
         if (lane < K)
           __hip_atomic_fetch_add(&a.slots[(row_base + (s - gen_start)) * ks + lane],
-                                 (1ull << 44) + (unsigned long long)(long long)mine, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+                                 ((unsigned long long)(kgen + 1) << 44) + (unsigned long long)(long long)mine,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ++my_evals;
       }
     }
@@ -2561,6 +2580,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
     const unsigned long long selm = s_ring[stop & (D - 1)];
     if (threadIdx.x < kStreamClauses) s_selj[threadIdx.x] = ((selm >> threadIdx.x) & 1ull) ? 0 : -1;
     if (threadIdx.x == 0) s_ntask = 0;
+    for (int j = threadIdx.x; j < K * kStreamClauses; j += blockDim.x) s_wt_old[j] = s_wt[j];
     ++my_stops;
     __syncthreads();
     {
@@ -2630,9 +2650,67 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       if (lane == 0) s_ninc[idx] = exact_count ? cnt : (cnt > 0);
     }
     if (wave == 0 && lane < n_own) s_pw[lane] += (int)((selm >> lane) & 1ull);  // the stop sample's
-    row_base += (int64_t)(stop + 1 - gen_start) + D;
-    depth0 = 2 * (stop + 1 - gen_start) < D ? (2 * (stop + 1 - gen_start) > 2 ? 2 * (stop + 1 - gen_start) : 2) : D;
-    gen_start = stop + 1;
+    depth0 = 2 * (stop + 1 - next) < D ? (2 * (stop + 1 - next) > 2 ? 2 * (stop + 1 - next) : 2) : D;
+    next = stop + 1;
+    if (kgen < kgen_cap) {
+      // The stream goes on past the stop.  Every row this workgroup published past it was
+      // evaluated with the state before the feedback; only the updated clauses' votes
+      // differ now, so the row gets their difference as this workgroup's next unit, and a
+      // row published from here on carries kgen + 1 units at once.
+      ++kgen;
+      __syncthreads();  // include counts of the updated clauses
+      for (int q = wave; q < D; q += nwv) {
+        const int r = s_pub[q];
+        if (r < next) continue;  // consumed (or none)
+        // bit tk: updated clause s_task_idx[tk] has an included literal that is 0 in sample r
+        // (the sample's complemented words are kept in its ring slot)
+        unsigned long long badm = 0ull;
+        const uint32_t* nxr = s_nx + (int64_t)q * Wp;
+        for (int64_t w0 = 0; w0 < g.W; w0 += kWave) {
+          const int64_t w = w0 + lane;
+          const uint32_t nxw = w < g.W ? nxr[w] : 0u;
+          for (int tk = 0; tk < ntask; ++tk) {
+            const uint32_t mw = w < g.W ? s_planes[s_task_idx[tk] * cw + (int64_t)(g.np - 1) * g.W + w] : 0u;
+            if (__any((mw & nxw) != 0u)) badm |= 1ull << tk;
+          }
+        }
+        // lane tk: the updated clause's selection for sample r (fast_eval and the rank-1
+        // draw of select_active, as in the evaluation above)
+        bool nsel = false;
+        if (lane < ntask) {
+          const int idx = s_task_idx[lane];
+          if (s_ninc[idx] == 0 || ((badm >> lane) & 1ull) == 0ull)
+            nsel = uniform_from_word(
+                       counted_site(a, a.step0 + (uint64_t)r, (uint32_t)(c_begin + idx), TAG_SEL, 0u).x) < 1.0f;
+        }
+        const unsigned long long nb = __ballot(nsel);
+        unsigned long long chg = 0ull, nsm = 0ull;
+        for (int tk = 0; tk < ntask; ++tk) {
+          const int idx = s_task_idx[tk];
+          chg |= 1ull << idx;
+          nsm |= ((nb >> tk) & 1ull) << idx;
+        }
+        const unsigned long long om = s_ring[q];
+        if (lane < K) {
+          long long delta = 0;
+          for (int tk = 0; tk < ntask; ++tk) {
+            const int idx = s_task_idx[tk];
+            if ((nsm >> idx) & 1ull) delta += s_wt[lane * kStreamClauses + idx];
+            if ((om >> idx) & 1ull) delta -= s_wt_old[lane * kStreamClauses + idx];
+          }
+          __hip_atomic_fetch_add(&a.slots[(row_base + (r - gen_start)) * ks + lane],
+                                 (1ull << 44) + (unsigned long long)delta, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lane == 0) s_ring[q] = (om & ~chg) | nsm;
+      }
+    } else {
+      // a fresh stream on fresh rows: the rows published past the stop are never read
+      row_base += (int64_t)(next - gen_start) + D;
+      gen_start = next;
+      kgen = 0;
+      for (int q = threadIdx.x; q < D; q += blockDim.x) s_pub[q] = -1;
+    }
     __syncthreads();
     if (prof) {
       const uint64_t now = __builtin_amdgcn_s_memrealtime();

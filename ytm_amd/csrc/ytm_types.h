@@ -106,6 +106,7 @@ struct TrainArgs {
   int profile;               // accumulate per-phase times into counters[4..11]; 4: count draws instead
   int test_timeout;          // test hook: class-sum waits never see their sums and expire at once
   int xt_halves;             // XT's literals Lh..L-1 are the complements of 0..Lh-1 (checked per dataset)
+  int stream_gens;           // streaming kernel: stops per stream before fresh rows (0: as many as fit; test hook)
   Geom g;
 };
 
