@@ -38,6 +38,8 @@ struct ytm_model {
   void* d_sout = nullptr;
   void* d_slists = nullptr;
   size_t sacc_bytes = 0, sout_bytes = 0, slists_bytes = 0;
+  void* h_sout = nullptr;  // pinned host staging of the class sums (hipHostMalloc)
+  size_t h_sout_bytes = 0;
   // Upper bound of |clause weight|: 1 after initialisation, the largest loaded magnitude
   // after ytm_set_weights, and + 1 per trained sample (a sample moves a weight by at most 1).
   double w_bound = 1.0;
@@ -475,6 +477,7 @@ void ytm_destroy(ytm_model* m) {
                   m->d_counters, m->d_err, m->d_slots, m->d_sacc, m->d_sout, m->d_slists};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
+  if (m->h_sout) (void)hipHostFree(m->h_sout);
   if (m->ev0) (void)hipEventDestroy(m->ev0);
   if (m->ev1) (void)hipEventDestroy(m->ev1);
   if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -864,7 +867,8 @@ ScorePlan score_plan(const Geom& g, bool has_xt) {
 
 // Class sums of N samples (X [N][P][W], XT its literal-major copy or null) into out (device
 // float [N][K]), with the caller's buffers acc (plan.acc_per_sample * N bytes) and lists
-// (plan.lists_bytes).  Enqueued on the model's stream; the include counts are current.
+// (plan.lists_bytes).  Enqueued on the model's stream; the include counts are current when
+// the plan has no lists (the list-based scorers count the literals of their lists).
 hipError_t score_samples(ytm_model* m, const ScorePlan& plan, const uint32_t* X, const uint32_t* XT, int64_t N,
                          long long* acc, void* lists, float* out) {
   const Geom& g = m->g;
@@ -925,14 +929,26 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (e == hipSuccess && plan.lists_bytes) e = ensure_buffer(&m->d_slists, &m->slists_bytes, plan.lists_bytes);
   float* dout = (float*)m->d_sout;
   int rc = YTM_OK;
-  if (e == hipSuccess) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
+  // the include counts, for the scorers that read them (the list-based ones count their lists)
+  if (e == hipSuccess && !plan.lists_bytes) e = ytm::launch_ninc(m->d_planes, m->d_ninc, g, m->stream);
   if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
   if (e == hipSuccess)
     e = score_samples(m, plan, ds->d_X, ds->d_XT, N, (long long*)m->d_sacc, plan.lists_bytes ? m->d_slists : nullptr,
                       dout);
   if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(class_sums, dout, (size_t)(N * g.K) * 4, hipMemcpyDeviceToHost, m->stream);
+  // the sums come back through a pinned staging buffer of the model (a direct copy into
+  // pageable memory goes through the runtime's own staging, in smaller pieces)
+  const size_t out_bytes = (size_t)(N * g.K) * 4;
+  if (e == hipSuccess && m->h_sout_bytes < out_bytes) {
+    if (m->h_sout) (void)hipHostFree(m->h_sout);
+    m->h_sout = nullptr;
+    m->h_sout_bytes = 0;
+    e = hipHostMalloc(&m->h_sout, out_bytes, hipHostMallocDefault);
+    if (e == hipSuccess) m->h_sout_bytes = out_bytes;
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(m->h_sout, dout, out_bytes, hipMemcpyDeviceToHost, m->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  if (e == hipSuccess) std::memcpy(class_sums, m->h_sout, out_bytes);
   float ms = 0.0f;
   if (e == hipSuccess) e = hipEventElapsedTime(&ms, m->ev0, m->ev1);
   if (e != hipSuccess) rc = fail(YTM_EHIP, std::string("score failed: ") + hipGetErrorString(e));
