@@ -205,12 +205,12 @@ def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=No
                 f"q-skip/update {d[1] / N:.0f} literal {d[2] / N:.0f}")
         elif os.environ.get("YTM_TRAIN_PROFILE"):
             names = {0: ("exchange", "barrier", "D1", "barrier", "D2", "D3+re-eval", "barrier", "step1-slowest-wave"),
-                     3: ("stream", "drain", "decide", "apply")}.get(
+                     3: ("stream", "drain", "decide", "apply", "first-row")}.get(
                          ep["kind"], ("stage", "publish+exchange", "next-A-wait", "decide", "apply", "re-eval"))
             log("[bench]   phase us/sample (wave 0): " + " ".join(f"{n} {v:.2f}" for n, v in zip(names, ep["phase"])))
             if ep["kind"] == 3 and ep["feedback"]:
                 log("[bench]   per stop, us: " + " ".join(f"{n} {v * N / ep['feedback']:.2f}"
-                                                       for n, v in zip(names[1:], ep["phase"][1:4])))
+                                                       for n, v in zip(names[1:], ep["phase"][1:5])))
     timed = epochs[warmup:]
 
     # inference over the test set (resident), best of 3 after one warm call

@@ -2390,10 +2390,11 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
     if (lane == 0) s_ninc[idx] = exact_count ? cnt : (cnt > 0);
   }
 
-  // Profile (a.profile, wave 0's view, summed into counters[4..7]): streaming, draining the
-  // evaluation waves after a stop, feedback decisions, literal updates.
+  // Profile (a.profile, wave 0's view, summed into counters[4..8]): streaming, draining the
+  // evaluation waves after a stop, feedback decisions, literal updates and repairs, and
+  // (within streaming) the wait for each phase's first row after a stop.
   const bool prof = a.profile && wave == 0;
-  uint64_t prof_acc[4] = {0, 0, 0, 0};
+  uint64_t prof_acc[5] = {0, 0, 0, 0, 0};
   uint64_t prof_last = t_kernel;
   int gen_start = 0;  // first sample of the stream (row row_base)
   int64_t row_base = 0;
@@ -2422,6 +2423,8 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       const long long bias_k = (long long)a.bias[k];
       int j = next;
       int stop = -1;
+      bool first_row = next > 0;  // profile: the wait for a phase's first row after a stop
+      const uint64_t t_phase = __builtin_amdgcn_s_memrealtime();
       // a count no word reaches under the test hook: every wait then expires
       const unsigned long long units = (unsigned long long)G * (unsigned long long)(kgen + 1);
       const unsigned long long complete = units + (a.test_timeout ? 1ull : 0ull);
@@ -2458,6 +2461,10 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           __builtin_amdgcn_s_sleep(1);
         }
         wait_ticks += __builtin_amdgcn_s_memrealtime() - t0;
+        if (prof && first_row) {
+          prof_acc[4] += __builtin_amdgcn_s_memrealtime() - t_phase;
+          first_row = false;
+        }
         if (ncomp == 0) break;  // aborted
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // the rows' LDS rings are written
         // feedback possible in row q?  prob > 0 for some class (class_fb, kernel.cu:508-529)
@@ -2659,7 +2666,9 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       // row published from here on carries kgen + 1 units at once.
       ++kgen;
       __syncthreads();  // include counts of the updated clauses
-      for (int q = wave; q < D; q += nwv) {
+      // in row order from the next row, which the consumer waits for first
+      for (int u = wave; u < D; u += nwv) {
+        const int q = (next + u) & (D - 1);
         const int r = s_pub[q];
         if (r < next) continue;  // consumed (or none)
         // bit tk: updated clause s_task_idx[tk] has an included literal that is 0 in sample r
@@ -2729,7 +2738,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
     atomicAdd(&a.counters[2], (unsigned long long)(__builtin_amdgcn_s_memrealtime() - t_kernel));
     if (wg == 0) atomicAdd(&a.counters[12], my_stops);
     if (prof)
-      for (int j = 0; j < 4; ++j) atomicAdd(&a.counters[4 + j], (unsigned long long)prof_acc[j]);
+      for (int j = 0; j < 5; ++j) atomicAdd(&a.counters[4 + j], (unsigned long long)prof_acc[j]);
   }
 }
 
