@@ -1141,11 +1141,11 @@ size_t stream_lds_bytes(const Geom& g, int threads) {
   // layout of train_stream_body: task masks [64][3] u64; planes [64][np][W]; weights [64][K]
   // f32 and [K][64] i32; include counts, drop, patch weights, task clauses, zeros, stop
   // selections [64] i32 each; targets ring [depth][K]; complemented samples ring [depth][Wp];
-  // integer weights before a stop [K][64]
+  // integer weights before a stop [K][64]; word-major include masks [Wp][64]
   (void)threads;
   const size_t C = kStreamClauses, K = (size_t)g.K, Wp = (size_t)((g.W + 3) & ~(int64_t)3);
   return 3 * C * 8 + C * (size_t)g.np * (size_t)g.W * 4 + 2 * C * K * 4 + 6 * C * 4 + (size_t)kStreamDepth * K * 4 +
-         (size_t)kStreamDepth * Wp * 4 + K * C * 4;
+         (size_t)kStreamDepth * Wp * 4 + K * C * 4 + Wp * C * 4;
 }
 
 static const void* train_fn(TrainKind kind, bool inject) {

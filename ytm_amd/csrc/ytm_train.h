@@ -1200,7 +1200,7 @@ __device__ __forceinline__ void global_phase_a(const TrainArgs& a, const Geom& g
 // literal-major buffer serves; the words of samples i and i+1 (mask_lds) take two.
 template <bool VANILLA, bool INJECT>
 __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom& g) {
-  extern __shared__ long long dyn_lds[];
+  extern __shared__ __attribute__((aligned(16))) long long dyn_lds[];  // 16-byte aligned: uint4 accesses
   __shared__ long long s_part[2][64];  // partial class sums by sample parity
   __shared__ int s_tgt[64];
   __shared__ double s_prob[64];
@@ -1819,7 +1819,7 @@ __device__ __forceinline__ void commit_fused_task(const TrainArgs& a, const Geom
 // change.  Samples, draws and selections are multi-buffered by sample index.
 template <bool INJECT>
 __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Geom& g) {
-  extern __shared__ long long dyn_lds[];
+  extern __shared__ __attribute__((aligned(16))) long long dyn_lds[];  // 16-byte aligned: uint4 accesses
   __shared__ long long s_part[2][64];  // partial class sums of samples i and i+1
   __shared__ int s_tgt[64];
   __shared__ double s_prob[64];
@@ -2330,7 +2330,7 @@ __device__ __forceinline__ void lds_store(int* p, int v) {
 }
 
 __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom& g) {
-  extern __shared__ long long dyn_lds[];
+  extern __shared__ __attribute__((aligned(16))) long long dyn_lds[];  // 16-byte aligned: uint4 accesses
   __shared__ StreamCtl ctl;
   __shared__ unsigned long long s_ring[kStreamDepth];  // selected clauses of in-flight samples
   __shared__ int s_pub[kStreamDepth];                  // the sample of each ring slot this workgroup published
@@ -2349,7 +2349,8 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   // LDS (sizes in stream_lds_bytes): task masks [64][3] u64; planes [64][np][W]; weights
   // [64][K]; transposed integer weights [K][64]; include counts, drop, patch weights, task
   // clauses, zeros, selections of the stop sample [64] each; targets ring [D][K];
-  // complemented samples ring [D][Wp]; integer weights before a stop [K][64].
+  // complemented samples ring [D][Wp]; integer weights before a stop [K][64]; the include
+  // masks again, word-major [Wp / 4][64] uint4 (lane = clause, four words per read).
   unsigned long long* s_task_m = (unsigned long long*)dyn_lds;
   uint32_t* s_planes = (uint32_t*)(s_task_m + 3 * kStreamClauses);
   float* s_w = (float*)(s_planes + (int64_t)kStreamClauses * cw);
@@ -2363,6 +2364,16 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   int32_t* s_yring = s_selj + kStreamClauses;
   uint32_t* s_nx = (uint32_t*)(s_yring + D * K);
   int* s_wt_old = (int*)(s_nx + (int64_t)D * Wp);  // [K][64] integer weights before a stop
+  uint4* s_maskT = (uint4*)(s_wt_old + K * kStreamClauses);
+  const int64_t Wq = Wp / 4;
+  // word group w4 of clause idx's include mask (zero past W and past the own clauses)
+  auto mask_quad = [&](int idx, int64_t w4) -> uint4 {
+    const uint32_t* mt = s_planes + idx * cw + (int64_t)(g.np - 1) * g.W;
+    const int64_t w = 4 * w4;
+    const bool ok = idx < n_own;
+    return uint4{ok && w < g.W ? mt[w] : 0u, ok && w + 1 < g.W ? mt[w + 1] : 0u, ok && w + 2 < g.W ? mt[w + 2] : 0u,
+                 ok && w + 3 < g.W ? mt[w + 3] : 0u};
+  };
   const bool exact_count = g.maxinc < g.L;
   const int ks = (K + 15) & ~15;
   unsigned long long my_updates = 0ull, my_evals = 0ull, my_stops = 0ull;
@@ -2381,6 +2392,8 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
     s_zero[j] = 0;
   }
   __syncthreads();
+  for (int64_t j = threadIdx.x; j < Wq * kStreamClauses; j += blockDim.x)
+    s_maskT[j] = mask_quad((int)(j % kStreamClauses), j / kStreamClauses);
   // include counts (or emptiness when MAX_INCLUDED_LITERALS >= L), one clause per wave
   for (int idx = wave; idx < n_own; idx += nwv) {
     const uint32_t* m = s_planes + idx * cw + (int64_t)(g.np - 1) * g.W;
@@ -2494,7 +2507,6 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
     } else {
       // ---- evaluation: claim samples in order, evaluate with the current state, publish
       const bool own = lane < n_own;
-      const uint32_t* m = s_planes + (int64_t)(own ? lane : 0) * cw + (int64_t)(g.np - 1) * g.W;
       for (;;) {
         if (lds_load(&ctl.stop) >= 0) break;
         int s = 0;
@@ -2537,7 +2549,12 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         __builtin_amdgcn_wave_barrier();
         // fast_eval (kernel.cu:255-282): an empty clause fires in training
         uint32_t bad = 0u;
-        for (int64_t w = 0; w < g.W; ++w) bad |= m[w] & nx[w];
+        const uint4* nx4 = (const uint4*)nx;
+#pragma unroll 2
+        for (int64_t w4 = 0; w4 < Wq; ++w4) {
+          const uint4 mv = s_maskT[w4 * kStreamClauses + lane], xv = nx4[w4];
+          bad |= (mv.x & xv.x) | (mv.y & xv.y) | (mv.z & xv.z) | (mv.w & xv.w);
+        }
         const bool fire = own && s_drop[lane] == 0 && (s_ninc[lane] == 0 || bad == 0u);
         // a stop set meanwhile lies before s: its row will not be read
         if (lds_load(&ctl.stop) >= 0) break;
@@ -2655,6 +2672,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       for (int64_t w = lane; w < g.W; w += kWave) cnt += __popc(mt[w]);
       cnt = wave_sum_i32(cnt);
       if (lane == 0) s_ninc[idx] = exact_count ? cnt : (cnt > 0);
+      for (int64_t w4 = lane; w4 < Wq; w4 += kWave) s_maskT[w4 * kStreamClauses + idx] = mask_quad(idx, w4);
     }
     if (wave == 0 && lane < n_own) s_pw[lane] += (int)((selm >> lane) & 1ull);  // the stop sample's
     depth0 = 2 * (stop + 1 - next) < D ? (2 * (stop + 1 - next) > 2 ? 2 * (stop + 1 - next) : 2) : D;
