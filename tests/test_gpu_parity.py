@@ -185,6 +185,35 @@ def test_fit_stream_launch_shapes(monkeypatch, wgs, threads, gens):
         assert_state_equal(tm, ref, f"epoch {epoch}")
 
 
+@pytest.mark.parametrize("classes,wlim", [(10, 50), (10, 511), (10, 512), (3, 300), (3, 3000)])
+def test_stream_votes_with_large_weights(monkeypatch, classes, wlim):
+    """The streaming kernel sums two classes' votes in one 32-bit reduction while every own
+    clause's |weight| is below 512, and one class at a time otherwise (an odd class count
+    leaves one class alone either way).  Weights drawn from [-wlim, wlim] put the workgroups
+    on either side of that bound; both against the oracle."""
+    monkeypatch.setenv("YTM_TRAIN_STREAM", "1")
+    kw = dict(number_of_clauses_per_class=120, T=400, s=4.0, dim=(40, 1, 1), n_classes=classes, seed=13)
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(120, 400, 4.0, (40, 1, 1), classes, seed=13)
+    rng = np.random.default_rng(wlim)
+    X = (rng.random((600, 40)) < 0.5).astype(np.uint32)
+    y = rng.integers(0, classes, size=600).astype(np.uint32)
+    ta = tm.get_ta_state().reshape(ref.ta.shape)
+    w = rng.integers(-wlim, wlim + 1, ref.w.shape).astype(np.float32)
+    tm.load_state_dict({"state": {"ta_state": ta, "clause_weights": w,
+                                  "patch_weights": np.zeros(ref.pw.shape, dtype=np.int32),
+                                  "min_y": None, "max_y": None}})
+    ref.w[...] = w
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    for epoch in range(2):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, encY)
+        assert tm.stats()["train_kind"] == 3
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+
+
 def test_specialised_kernel_is_used():
     tm, ref, X, y, *_ = pair(2, 20)
     tm.fit(tm.encode(X), y, is_X_encoded=True)

@@ -2334,6 +2334,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   __shared__ StreamCtl ctl;
   __shared__ unsigned long long s_ring[kStreamDepth];  // selected clauses of in-flight samples
   __shared__ int s_pub[kStreamDepth];                  // the sample of each ring slot this workgroup published
+  __shared__ int s_wmax;                               // bound on |integer weight| of the own clauses
   __shared__ long long s_S[64];                        // class sums + bias of the stop sample
   __shared__ int s_ntask;
   const int lane = lane_id();
@@ -2380,11 +2381,14 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
 
+  if (threadIdx.x == 0) s_wmax = 0;
+  __syncthreads();
   for (int64_t j = threadIdx.x; j < n_own * cw; j += blockDim.x) s_planes[j] = a.planes[c_begin * cw + j];
   for (int64_t j = threadIdx.x; j < n_own * K; j += blockDim.x) {
     const float w = a.weights[c_begin * K + j];
     s_w[j] = w;
     s_wt[(j % K) * kStreamClauses + j / K] = (int)w;
+    atomicMax(&s_wmax, (int)w < 0 ? -(int)w : (int)w);
   }
   for (int j = threadIdx.x; j < kStreamClauses; j += blockDim.x) {
     s_drop[j] = j < n_own ? a.drop[c_begin + j] == 1u : 1;
@@ -2436,6 +2440,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       const long long bias_k = (long long)a.bias[k];
       int j = next;
       int stop = -1;
+      int pw_add = 0;
       bool first_row = next > 0;  // profile: the wait for a phase's first row after a stop
       const uint64_t t_phase = __builtin_amdgcn_s_memrealtime();
       // a count no word reaches under the test hook: every wait then expires
@@ -2490,11 +2495,9 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         }
         const unsigned long long fbm = __ballot(fb);
         const int qf = fbm ? (__ffsll((long long)fbm) - 1) / K : ncomp;  // first row with feedback
-        // patch weights of the rows before it (select_active, kernel.cu:305)
-        for (int r = 0; r < qf; ++r) {
-          const unsigned long long sm = s_ring[(j + r) & (D - 1)];
-          if (lane < n_own) s_pw[lane] += (int)((sm >> lane) & 1ull);
-        }
+        // patch weights of the rows before it (select_active, kernel.cu:305), counted in a
+        // register of the clause's lane and added to LDS when the phase ends
+        for (int r = 0; r < qf; ++r) pw_add += (int)((s_ring[(j + r) & (D - 1)] >> lane) & 1ull);
         if (qf < ncomp) {
           if (q == qf) s_S[k] = S;
           stop = j + qf;
@@ -2503,6 +2506,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         j += ncomp;
         if (lane == 0) lds_store(&ctl.consume, j);
       }
+      if (lane < n_own) s_pw[lane] += pw_add;
       if (lane == 0) lds_store(&ctl.stop, stop >= 0 ? stop : a.N);
     } else {
       // ---- evaluation: claim samples in order, evaluate with the current state, publish
@@ -2567,11 +2571,25 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         }
         const unsigned long long smask = __ballot(sel);
         int mine = 0;
-        if (smask)
-          for (int kk = 0; kk < K; ++kk) {
+        if (smask) {
+          // Two classes per 32-bit sum while |weight| < 512: each selected lane adds w + 512
+          // (1 .. 1023) into a 16-bit field, so 64 lanes stay below 2^16 and no field carries
+          // into the next; the bias of the selected lanes comes off again.
+          int kk = 0;
+          if (lds_load(&s_wmax) < 512) {
+            const int nbias = 512 * __popcll(smask);
+            for (; kk + 1 < K; kk += 2) {
+              const int v0 = s_wt[kk * kStreamClauses + lane] + 512, v1 = s_wt[(kk + 1) * kStreamClauses + lane] + 512;
+              const int p = wave_sum_i32(sel ? (v0 | (v1 << 16)) : 0);
+              if (lane == kk) mine = (p & 0xFFFF) - nbias;
+              if (lane == kk + 1) mine = (int)((unsigned)p >> 16) - nbias;
+            }
+          }
+          for (; kk < K; ++kk) {
             const int p = wave_sum_i32(sel ? s_wt[kk * kStreamClauses + lane] : 0);
             if (lane == kk) mine = p;
           }
+        }
         if (lane == 0) {
           s_ring[s & (D - 1)] = smask;
           s_pub[s & (D - 1)] = s;
@@ -2626,6 +2644,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         if (valid && (po.t1a || po.t2)) {
           s_w[ix * K + kk] = po.w_new;
           s_wt[kk * kStreamClauses + ix] = (int)po.w_new;
+          atomicMax(&s_wmax, (int)po.w_new < 0 ? -(int)po.w_new : (int)po.w_new);
         }
         const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
         if ((b1a | b1b | bt2) == 0ull) continue;
