@@ -214,6 +214,38 @@ def test_stream_votes_with_large_weights(monkeypatch, classes, wlim):
         assert_state_equal(tm, ref, f"epoch {epoch}")
 
 
+@pytest.mark.parametrize("env", [dict(YTM_TRAIN_STREAM="1"), dict(YTM_TRAIN_STREAM="0"),
+                                 dict(YTM_TRAIN_STREAM="0", YTM_TRAIN_GLOBAL="1")])
+def test_rank1_draw_of_exactly_one(monkeypatch, env):
+    """With one patch a firing clause is selected unless its reservoir draw is exactly 1.0
+    (u < 1.0f / 1, kernel.cu:295-301), which happens once in 2^24 draws of the counter stream.
+    Seed 6589 has that draw at step 58 for clause 28, among the first steps of a fresh model:
+    the streaming, resident and global one-patch kernels against the oracle."""
+    ctr_word = orc.philox4x32_10([58, 28, 1 << 28, 0], [6589, 0])[0]
+    assert (int(ctr_word) >> 8) == 0xFFFFFF  # site (t=58, c=28, SEL, 0), word 0: u = 1.0
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    kw = dict(number_of_clauses_per_class=64, T=10, s=3.9, dim=(16, 1, 1), n_classes=2, seed=6589)
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(64, 10, 3.9, (16, 1, 1), 2, seed=6589)
+    rng = np.random.default_rng(1)
+    X = (rng.random((100, 16)) < 0.5).astype(np.uint32)
+    y = rng.integers(0, 2, size=100).astype(np.uint32)
+    encX = tm.encode(X)
+    # clause 28 fires on sample 58 after the first 58 steps: the rejected draw decides its selection
+    pre = orc.OracleTM(64, 10, 3.9, (16, 1, 1), 2, seed=6589)
+    pre.fit_encoded(encX[:58], pre.encode_y_multiclass(y[:58]))
+    inc = pre.ta.reshape(64, -1)[28] > tm.number_of_ta_states // 2
+    bits = np.unpackbits(encX[58].reshape(-1).view(np.uint8), bitorder="little")[:inc.size]
+    assert np.all(bits[inc] == 1)
+    tm.fit(encX, y, is_X_encoded=True)
+    upd = ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+    want = 3 if env["YTM_TRAIN_STREAM"] == "1" else (1 if "YTM_TRAIN_GLOBAL" in env else 0)
+    assert tm.stats()["train_kind"] == want
+    assert tm.stats()["last_fit_updates"] == upd
+    assert_state_equal(tm, ref)
+
+
 def test_specialised_kernel_is_used():
     tm, ref, X, y, *_ = pair(2, 20)
     tm.fit(tm.encode(X), y, is_X_encoded=True)
