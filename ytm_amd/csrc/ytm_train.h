@@ -2421,8 +2421,10 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   // below 2^19); a.stream_gens lowers it (test hook).
   int kgen_cap = (1 << 19) / G - 2;
   if (a.stream_gens > 0 && a.stream_gens < kgen_cap) kgen_cap = a.stream_gens;
-  // Lookahead at the start of a phase: twice the previous phase's length (2 to D), so that
-  // speculation stays shallow while stops are frequent and is deep as soon as they are rare.
+  // Lookahead at the start of a phase: 2 after a phase of one sample (a stop at every sample),
+  // else eight times the previous phase's length, at most D: deep as soon as stops are a few
+  // samples apart (the rows published past a stop are repaired, not discarded, so depth
+  // costs little then).
   int depth0 = 2;
   for (int q = threadIdx.x; q < D; q += blockDim.x) s_pub[q] = -1;
   while (next < a.N) {
@@ -2694,7 +2696,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       for (int64_t w4 = lane; w4 < Wq; w4 += kWave) s_maskT[w4 * kStreamClauses + idx] = mask_quad(idx, w4);
     }
     if (wave == 0 && lane < n_own) s_pw[lane] += (int)((selm >> lane) & 1ull);  // the stop sample's
-    depth0 = 2 * (stop + 1 - next) < D ? (2 * (stop + 1 - next) > 2 ? 2 * (stop + 1 - next) : 2) : D;
+    depth0 = stop == next ? 2 : (8 * (stop + 1 - next) < D ? 8 * (stop + 1 - next) : D);
     next = stop + 1;
     if (kgen < kgen_cap) {
       // The stream goes on past the stop.  Every row this workgroup published past it was
