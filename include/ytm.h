@@ -86,7 +86,7 @@ typedef struct ytm_stats {
     int32_t train_kind;          /* 0 = clause state resident in LDS, 1 = global (one
                                     patch), 2 = global (several patches), 3 = resident and
                                     streaming (one patch), 4 = clause banks (coalesced=0):
-                                    two ordinary launches per sample */
+                                    one ordinary launch per sample */
     int32_t train_specialised;   /* 1 when the last fit ran a training kernel compiled at run
                                     time for this model's geometry (hipRTC), 0 when it ran the
                                     built-in kernel (YTM_JIT=0, or the compile was unavailable) */

@@ -311,9 +311,9 @@ ytm::TrainKind choose_train_kind(Geom* g, int cpw, bool force_global) {
   return kind;
 }
 
-// fit() of a clause-bank model (coalesced=False): two ordinary launches per sample
-// (launch_bank_sample), no persistent kernel and no wait between workgroups.  Slot memory:
-// the class sums of two consecutive samples [2][64] int64, then sel [C] and ninc [C].
+// fit() of a clause-bank model (coalesced=False): one ordinary launch per sample plus one
+// (launch_bank_step), no persistent kernel and no wait between workgroups.  Slot memory:
+// three class-sum rows [3][64] int64, then sel [C] and ninc [C].
 int fit_banks(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count, const uint32_t* drop,
               const float* inject) {
   const Geom& g = m->g;
@@ -321,10 +321,10 @@ int fit_banks(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count,
   const int64_t block = g.C * g.P + 2 * g.C * g.K + g.C * g.K * g.L;
   int64_t chunk = count;  // samples per copy of the injected blocks (<= 1 GiB)
   if (inj) chunk = std::min<int64_t>(chunk, std::max<int64_t>(1, ((int64_t)1 << 30) / (block * 4)));
-  int rc = ensure_slots(m, (size_t)(2 * 64 * 8 + g.C * 8));
+  int rc = ensure_slots(m, (size_t)(3 * 64 * 8 + g.C * 8));
   if (rc) return rc;
   long long* sums = (long long*)m->d_slots;
-  int* d_sel = (int*)(sums + 2 * 64);
+  int* d_sel = (int*)(sums + 3 * 64);
   int* d_ninc = d_sel + g.C;
   uint32_t* d_drop = nullptr;
   float* d_inj = nullptr;
@@ -355,7 +355,6 @@ int fit_banks(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count,
       return finish(fail(YTM_EHIP, std::string(#expr) + " failed: " + hipGetErrorString(e_)));  \
   } while (0)
   BANK_TRY(hipMemsetAsync(m->d_counters, 0, 128, m->stream));
-  BANK_TRY(ytm::launch_fill_u64((unsigned long long*)sums, 2 * 64, m->stream));
   m->w_bound += (double)count;
   double ms_total = 0.0;
   int launches = 0;
@@ -381,17 +380,14 @@ int fit_banks(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count,
     a.N = (int)n;
     a.g = g;
     BANK_TRY(hipEventRecord(m->ev0, m->stream));
-    for (int64_t i = 0; i < n; ++i) {
-      const int row = (int)((s + i) & 1);
-      BANK_TRY(ytm::launch_bank_sample(a, (int)i, sums + row * 64, sums + (row ^ 1) * 64, d_sel, d_ninc, inj,
-                                       m->stream));
-    }
+    BANK_TRY(ytm::launch_fill_u64((unsigned long long*)sums, 3 * 64, m->stream));
+    for (int64_t i = 0; i <= n; ++i) BANK_TRY(ytm::launch_bank_step(a, (int)i, sums, d_sel, d_ninc, inj, m->stream));
     BANK_TRY(hipEventRecord(m->ev1, m->stream));
     BANK_TRY(hipEventSynchronize(m->ev1));
     float ms = 0.0f;
     BANK_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
     ms_total += ms;
-    launches += (int)(2 * n);
+    launches += (int)(n + 1);
   }
   unsigned long long cnt[16] = {0};
   BANK_TRY(hipMemcpy(cnt, m->d_counters, sizeof(cnt), hipMemcpyDeviceToHost));

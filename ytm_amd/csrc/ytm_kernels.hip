@@ -721,83 +721,77 @@ __global__ __launch_bounds__(kTrainThreads) void train_resident_kernel(TrainArgs
 __global__ __launch_bounds__(kTrainThreads) void train_stream_kernel(TrainArgs a) { train_stream_body(a, a.g); }
 
 // Clause banks (coalesced=False: clause c votes for and learns only its bank's class
-// c / per_bank, kernel.cu:306-312,563-565) train one sample per pair of launches, one wave
-// per clause at a time.  bank_eval_kernel evaluates every clause on sample i (fast_eval and
-// select_active, kernel.cu:255-316), stores its selected patch and include count in sel /
-// ninc, counts the patch weight and adds the bank votes into sums[K] (int64);
-// bank_feedback_kernel takes the class targets from those totals and runs each clause's
-// feedback (clause_update, kernel.cu:531-613).  The launch boundary orders the two phases,
-// so no workgroup ever waits on another.  The feedback launch of sample i clears the sums
-// row of sample i+1 (sums_next), which nothing reads before the next evaluation.
+// c / per_bank, kernel.cu:306-312,563-565) train with one ordinary launch per sample, a wave
+// per clause at a time.  Launch i runs, for each clause, the feedback of sample i-1
+// (clause_update, kernel.cu:531-613, from the class totals the previous launch completed)
+// and then the evaluation of sample i (fast_eval and select_active, kernel.cu:255-316),
+// which needs only the clause's own state: its selected patch and include count go to
+// sel / ninc, its patch weight is counted and its bank vote added into sample i's class-sum
+// row (int64).  The launch boundary orders the samples, so no workgroup ever waits on
+// another.  Rows cycle through three: launch i reads row (i-1) % 3, adds into row i % 3 and
+// clears row (i+1) % 3, which the previous launch read and the next one adds into.  Launch 0
+// only evaluates and launch N only applies feedback.
 template <bool ONE_PATCH, bool INJECT>
-__global__ __launch_bounds__(256) void bank_eval_kernel(TrainArgs a, int i, long long* __restrict__ sums,
+__global__ __launch_bounds__(256) void bank_step_kernel(TrainArgs a, int i, long long* __restrict__ rows,
                                                         int* __restrict__ sel, int* __restrict__ ninc) {
   const Geom& g = a.g;
   __shared__ long long s_part[64];
-  const int lane = lane_id();
-  const int64_t wave0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-  const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
-  if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
-  __syncthreads();
-  const uint64_t t = a.step0 + (uint64_t)i;
-  const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
-  const uint32_t* xe = a.X + (int64_t)i * g.P * g.W;
-  const int64_t cw = (int64_t)g.np * g.W;
-  for (int64_t c = wave0; c < g.C; c += nwaves) {
-    const uint32_t* m = a.planes + c * cw + (int64_t)(g.np - 1) * g.W;
-    int n = 0;
-    const int sl = eval_select<ONE_PATCH, INJECT>(a, g, inj, c, t, m, xe, a.drop[c] == 1u, 0.0f, &n);
-    if (lane == 0) {
-      sel[c] = sl;
-      ninc[c] = n;
-      if (sl >= 0) {
-        const int64_t k = c / g.per_bank;
-        a.patch_w[c * g.P + sl] += 1;
-        atomicAdd((unsigned long long*)&s_part[k], (unsigned long long)(long long)a.weights[c * g.K + k]);
-      }
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < g.K && s_part[threadIdx.x] != 0)
-    atomicAdd((unsigned long long*)&sums[threadIdx.x], (unsigned long long)s_part[threadIdx.x]);
-}
-
-template <bool INJECT>
-__global__ __launch_bounds__(256) void bank_feedback_kernel(TrainArgs a, int i, const long long* __restrict__ sums,
-                                                            long long* __restrict__ sums_next,
-                                                            const int* __restrict__ sel,
-                                                            const int* __restrict__ ninc) {
-  const Geom& g = a.g;
   __shared__ int s_tgt[64];
   __shared__ double s_prob[64];
   __shared__ unsigned long long s_upd;
   const int lane = lane_id();
-  if (threadIdx.x < g.K)
-    class_targets(g, (int)threadIdx.x, sums[threadIdx.x] + (long long)a.bias[threadIdx.x], a.Y + (int64_t)i * g.K,
-                  s_tgt, s_prob);
-  if (blockIdx.x == 0 && threadIdx.x < 64) sums_next[threadIdx.x] = 0;
+  const bool fb = i > 0, ev = i < a.N;
+  const long long* sums_prev = rows + ((i + 2) % 3) * 64;
+  long long* sums_cur = rows + (i % 3) * 64;
+  long long* sums_next = rows + ((i + 1) % 3) * 64;
+  if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_upd = 0ull;
+  if (fb && threadIdx.x < g.K)
+    class_targets(g, (int)threadIdx.x, sums_prev[threadIdx.x] + (long long)a.bias[threadIdx.x],
+                  a.Y + (int64_t)(i - 1) * g.K, s_tgt, s_prob);
+  if (blockIdx.x == 0 && threadIdx.x < 64) sums_next[threadIdx.x] = 0;
   __syncthreads();
-  if (blockIdx.x == 0 && threadIdx.x < kWave) {  // samples where some class may update
+  if (fb && blockIdx.x == 0 && threadIdx.x < kWave) {  // samples where some class may update
     const bool any = __ballot(lane < g.K && s_prob[lane < g.K ? lane : 0] > 0.0) != 0ull;
     if (lane == 0 && any) atomicAdd(&a.counters[12], 1ull);
   }
   const int64_t wave0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
-  const uint64_t t = a.step0 + (uint64_t)i;
-  const float* inj = INJECT ? a.inject + (int64_t)i * a.inject_block : nullptr;
-  const uint32_t* xe = a.X + (int64_t)i * g.P * g.W;
   const int64_t cw = (int64_t)g.np * g.W;
+  const uint64_t tp = a.step0 + (uint64_t)i - 1, t = a.step0 + (uint64_t)i;
+  const float* injp = INJECT && fb ? a.inject + (int64_t)(i - 1) * a.inject_block : nullptr;
+  const float* inj = INJECT && ev ? a.inject + (int64_t)i * a.inject_block : nullptr;
+  const uint32_t* xp = a.X + (int64_t)(fb ? i - 1 : 0) * g.P * g.W;
+  const uint32_t* xe = a.X + (int64_t)(ev ? i : 0) * g.P * g.W;
   for (int64_t c = wave0; c < g.C; c += nwaves) {
-    if (a.drop[c] == 1u) continue;  // a dropped clause gets no feedback (kernel.cu:555)
-    const int sl = sel[c];
-    const FbOps ops = decide<INJECT>(a, g, inj, c, t, sl, ninc[c], s_tgt, s_prob, a.weights + c * g.K, nullptr,
-                                     nullptr);
-    if ((ops.m1a | ops.m1b | ops.m2) == 0ull) continue;
-    apply_ops<INJECT>(a, g, inj, c, t, sl, ops, a.planes + c * cw, xe, nullptr);
-    if (lane == 0) atomicAdd(&s_upd, 1ull);
+    if (fb && a.drop[c] != 1u) {  // a dropped clause gets no feedback (kernel.cu:555)
+      const int sl = sel[c];
+      const FbOps ops = decide<INJECT>(a, g, injp, c, tp, sl, ninc[c], s_tgt, s_prob, a.weights + c * g.K, nullptr,
+                                       nullptr);
+      if ((ops.m1a | ops.m1b | ops.m2) != 0ull) {
+        apply_ops<INJECT>(a, g, injp, c, tp, sl, ops, a.planes + c * cw, xp, nullptr);
+        if (lane == 0) atomicAdd(&s_upd, 1ull);
+        __threadfence();  // the new planes (every lane's words) before the evaluation reads them
+      }
+    }
+    if (ev) {
+      const uint32_t* m = a.planes + c * cw + (int64_t)(g.np - 1) * g.W;
+      int n = 0;
+      const int sl = eval_select<ONE_PATCH, INJECT>(a, g, inj, c, t, m, xe, a.drop[c] == 1u, 0.0f, &n);
+      if (lane == 0) {
+        sel[c] = sl;
+        ninc[c] = n;
+        if (sl >= 0) {
+          const int64_t k = c / g.per_bank;
+          a.patch_w[c * g.P + sl] += 1;
+          atomicAdd((unsigned long long*)&s_part[k], (unsigned long long)(long long)a.weights[c * g.K + k]);
+        }
+      }
+    }
   }
   __syncthreads();
+  if (ev && threadIdx.x < g.K && s_part[threadIdx.x] != 0)
+    atomicAdd((unsigned long long*)&sums_cur[threadIdx.x], (unsigned long long)s_part[threadIdx.x]);
   if (threadIdx.x == 0 && s_upd) atomicAdd(&a.counters[0], s_upd);
 }
 
@@ -1174,22 +1168,18 @@ hipError_t launch_train(const TrainArgs& a, int grid, size_t lds_bytes, TrainKin
                                     (unsigned)lds_bytes, s);
 }
 
-hipError_t launch_bank_sample(const TrainArgs& a, int i, long long* sums, long long* sums_next, int* sel, int* ninc,
-                              bool inject, hipStream_t s) {
+hipError_t launch_bank_step(const TrainArgs& a, int i, long long* rows, int* sel, int* ninc, bool inject,
+                            hipStream_t s) {
   const int grid = grid_for(a.g.C * kWave, 256);
   const bool one = a.g.P == 1;
   if (one && inject)
-    bank_eval_kernel<true, true><<<grid, 256, 0, s>>>(a, i, sums, sel, ninc);
+    bank_step_kernel<true, true><<<grid, 256, 0, s>>>(a, i, rows, sel, ninc);
   else if (one)
-    bank_eval_kernel<true, false><<<grid, 256, 0, s>>>(a, i, sums, sel, ninc);
+    bank_step_kernel<true, false><<<grid, 256, 0, s>>>(a, i, rows, sel, ninc);
   else if (inject)
-    bank_eval_kernel<false, true><<<grid, 256, 0, s>>>(a, i, sums, sel, ninc);
+    bank_step_kernel<false, true><<<grid, 256, 0, s>>>(a, i, rows, sel, ninc);
   else
-    bank_eval_kernel<false, false><<<grid, 256, 0, s>>>(a, i, sums, sel, ninc);
-  if (inject)
-    bank_feedback_kernel<true><<<grid, 256, 0, s>>>(a, i, sums, sums_next, sel, ninc);
-  else
-    bank_feedback_kernel<false><<<grid, 256, 0, s>>>(a, i, sums, sums_next, sel, ninc);
+    bank_step_kernel<false, false><<<grid, 256, 0, s>>>(a, i, rows, sel, ninc);
   return hipGetLastError();
 }
 
