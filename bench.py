@@ -62,7 +62,8 @@ def load_traffic(config: int):
         return None
     try:
         d = json.loads(path.read_text())
-        return {"bytes_per_launch": float(d["bytes_per_launch"]), "kernel": d.get("kernel")}
+        return {"bytes_per_launch": float(d["bytes_per_launch"]), "kernel": d.get("kernel"),
+                "hbm_gbs": d.get("hbm_gbs")}
     except (KeyError, ValueError):
         return None
 
@@ -283,6 +284,11 @@ def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=No
     if traffic:
         res["roofline"]["traffic"] = traffic["bytes_per_launch"]
         res["roofline"]["traffic_kernel"] = traffic["kernel"]
+        if traffic["hbm_gbs"] is not None:
+            # the measured bytes of that launch over its own duration: the share of the HBM
+            # peak the kernel really uses (the byte model above counts reads it never makes)
+            res["roofline"]["traffic_gbs"] = traffic["hbm_gbs"]
+            res["roofline"]["traffic_frac"] = round(traffic["hbm_gbs"] / HBM_PEAK_GBS, 4)
     tm.release()
     if cpu_seconds > 0:
         res["cpu_baseline"] = cpu_baseline(cfg, kw, encX, y, encXt, cpu_seconds)
