@@ -348,6 +348,27 @@ def test_supported_limits(case):
     assert_packed_equal(tm.transform_patchwise(encX[:2], is_X_encoded=True, packed=True), ref_pw)
 
 
+def test_fit_conv_lists_of_literal_indices():
+    """Literal lists hold byte offsets into the literal-major sample only while those fit 16
+    bits; with 696 literals over 29 patch words ((L-1) * 4 * 29 > 65535) they hold literal
+    indices.  Training, scores and clause outputs against the oracle on that geometry."""
+    kw = dict(number_of_clauses_per_class=24, T=20, s=3.0, dim=(32, 32, 32), patch_dim=(3, 3), n_classes=2, seed=3)
+    tm = MultiClassTM(**kw)
+    assert (tm.number_of_literals - 1) * 4 * 29 > 0xFFFF
+    ref = orc.OracleTM(24, 20, 3.0, (32, 32, 32), 2, patch_dim=(3, 3), seed=3)
+    rng = np.random.default_rng(23)
+    X = (rng.random((12, 32 * 32 * 32)) < 0.5).astype(np.uint32)
+    y = rng.integers(0, 2, size=12).astype(np.uint32)
+    encX = tm.encode(X)
+    for epoch in range(3):
+        tm.fit(encX, y, is_X_encoded=True)
+        upd = ref.fit_encoded(encX, ref.encode_y_multiclass(y))
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+    np.testing.assert_array_equal(tm.score(encX, is_X_encoded=True), ref.score(encX))
+    np.testing.assert_array_equal(tm.transform(encX, is_X_encoded=True), ref.transform(encX))
+
+
 def test_fit_conv_variant_no_loc():
     tm, ref, X, y, *_ = pair(3, 30, clauses=50, encode_loc=False)
     encX = tm.encode(X)
@@ -528,6 +549,7 @@ def random_state(tm, ref, rng, include_p):
     ((1500, 1, 1), None, 2, 150),    # one patch, 94 words
     ((12, 12, 2), (4, 4), 4, 300),   # several patches, literal lists
     ((16, 16, 16), (3, 3), 3, 120),  # several patches, 340 literals: some clauses beyond the list capacity
+    ((32, 32, 32), (3, 3), 2, 40),   # 696 literals x 29 patch words: list entries are literal indices
 ])
 def test_inference_random_state(dim, patch_dim, classes, clauses):
     """Class sums and clause outputs on random states: every inference kernel variant

@@ -353,7 +353,9 @@ __global__ __launch_bounds__(256) void build_lists_kernel(const uint32_t* __rest
 // lv (the list padded to a multiple of 8).  With at least two groups of PW lanes in the wave
 // (the bitmap's PW words), group gq takes the runs 8(it * NG + gq) of step it, fetching
 // them from their lanes with ds_bpermute, and the groups' bitmaps are AND-ed at the end
-// (as firing_from_list); otherwise the runs are read 8 at a time with readlane.
+// (as firing_from_list); otherwise the runs are read 8 at a time with readlane.  SCALED:
+// the entries are byte offsets (lists_scaled).
+template <bool SCALED>
 __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 lv, int n, const uint32_t* xt,
                                                           uint32_t acc) {
   const int lane = lane_id();
@@ -372,15 +374,7 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
                              (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.y),
                              (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.z),
                              (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.w)};
-      if (in_group && run < nruns) {
-        uint32_t v = 0xFFFFFFFFu;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          v &= xt[(e[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)w];
-          v &= xt[(e[u] >> 16) * (uint32_t)PW + (uint32_t)w];
-        }
-        part &= v;
-      }
+      if (in_group && run < nruns) part &= and_listed_as<SCALED>(g, e, xt, (uint32_t)w);
       const unsigned long long live = __ballot(part != 0u);
       bool dead = false;
       for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * PW)) & gmask) == 0ull;
@@ -399,13 +393,7 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
     const int src = j >> 3;
     const uint32_t qv[4] = {(uint32_t)lane_value((int)lv.x, src), (uint32_t)lane_value((int)lv.y, src),
                             (uint32_t)lane_value((int)lv.z, src), (uint32_t)lane_value((int)lv.w, src)};
-    uint32_t v = 0xFFFFFFFFu;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      v &= xt[(qv[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)jl];
-      v &= xt[(qv[u] >> 16) * (uint32_t)PW + (uint32_t)jl];
-    }
-    acc &= v;
+    acc &= and_listed_as<SCALED>(g, qv, xt, (uint32_t)jl);
     if ((j & 8) && !__any(acc != 0u)) break;
   }
   return acc;
@@ -435,6 +423,7 @@ __global__ __launch_bounds__(kScoreLmThreads) void score_lm_kernel(const uint32_
   const int wave = threadIdx.x / kWave, nwv = blockDim.x / kWave;
   const int64_t xtw = g.L * ((g.P + 31) / 32);
   const int64_t nch = (g.C + kScoreLmChunk - 1) / kScoreLmChunk;
+  const bool scaled = lists_scaled(g);
   for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
     const int64_t e = blk / nch, ch = blk % nch;
     const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
@@ -448,7 +437,8 @@ __global__ __launch_bounds__(kScoreLmThreads) void score_lm_kernel(const uint32_
       uint32_t fire = all_patches_word(g);
       if (n <= kScoreListCap) {
         const uint4 lv = 8 * lane < n ? *(const uint4*)(lists + c * kScoreListCap + 8 * lane) : uint4{0u, 0u, 0u, 0u};
-        fire = firing_from_list_regs(g, lv, n, s_xts, fire);
+        fire = scaled ? firing_from_list_regs<true>(g, lv, n, s_xts, fire)
+                      : firing_from_list_regs<false>(g, lv, n, s_xts, fire);
       } else {
         fire = firing_from_mask(g, planes + (c * g.np + g.np - 1) * g.W, s_xts, fire);
       }
@@ -623,6 +613,7 @@ __global__ __launch_bounds__(kScoreLmThreads) void transform_lm_kernel(const uin
   const int PW = (int)((g.P + 31) / 32);
   const int64_t xtw = g.L * PW;
   const int64_t nch = (g.C + kScoreLmChunk - 1) / kScoreLmChunk;
+  const bool scaled = lists_scaled(g);
   for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
     const int64_t e = blk / nch, ch = blk % nch;
     const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
@@ -636,7 +627,8 @@ __global__ __launch_bounds__(kScoreLmThreads) void transform_lm_kernel(const uin
         if (n <= kScoreListCap) {
           const uint4 lv =
               8 * lane < n ? *(const uint4*)(lists + c * kScoreListCap + 8 * lane) : uint4{0u, 0u, 0u, 0u};
-          fire = firing_from_list_regs(g, lv, n, s_xts, fire);
+          fire = scaled ? firing_from_list_regs<true>(g, lv, n, s_xts, fire)
+                        : firing_from_list_regs<false>(g, lv, n, s_xts, fire);
         } else {
           fire = firing_from_mask(g, planes + (c * g.np + g.np - 1) * g.W, s_xts, fire);
         }

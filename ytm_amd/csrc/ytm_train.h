@@ -183,13 +183,54 @@ __device__ __forceinline__ uint32_t all_patches_word(const Geom& g) {
   return (lane == PW - 1 && (g.P & 31)) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu;
 }
 
+// A literal list entry of a model with several patches is the literal's byte offset in the
+// literal-major sample, l * 4 * ceil(P/32), when every such offset fits 16 bits: a list walk
+// then adds the entry to its lane's word address (one add, which reads the entry's half of
+// the packed pair in place) instead of multiplying it.  Otherwise, and for one-patch models,
+// the entry is the literal index l.
+__device__ __forceinline__ bool lists_scaled(const Geom& g) {
+  return g.P > 1 && (int64_t)(g.L - 1) * 4 * ((g.P + 31) / 32) <= 0xFFFF;
+}
+
+// AND of word `word` of the bitsets of the 2 * NE literals whose list entries e holds (two
+// per element) in the literal-major sample xt ([L][PW] words); SCALED: lists_scaled(g).
+template <bool SCALED, int NE>
+__device__ __forceinline__ uint32_t and_listed_as(const Geom& g, const uint32_t (&e)[NE], const uint32_t* xt,
+                                                  uint32_t word) {
+  uint32_t v = 0xFFFFFFFFu;
+  if (SCALED) {
+    const char* xb = (const char*)(xt + word);
+#pragma unroll
+    for (int u = 0; u < NE; ++u) {
+      v &= *(const uint32_t*)(xb + (e[u] & 0xFFFFu));
+      v &= *(const uint32_t*)(xb + (e[u] >> 16));
+    }
+  } else {
+    const uint32_t PW = (uint32_t)((g.P + 31) / 32);
+#pragma unroll
+    for (int u = 0; u < NE; ++u) {
+      v &= xt[(e[u] & 0xFFFFu) * PW + word];
+      v &= xt[(e[u] >> 16) * PW + word];
+    }
+  }
+  return v;
+}
+
+template <int NE>
+__device__ __forceinline__ uint32_t and_listed(const Geom& g, const uint32_t (&e)[NE], const uint32_t* xt,
+                                               uint32_t word) {
+  return lists_scaled(g) ? and_listed_as<true>(g, e, xt, word) : and_listed_as<false>(g, e, xt, word);
+}
+
 // Included literals of a clause (include mask m, W words), in increasing order, written to
-// list[0, n) when n <= cap, the entries from n to the next multiple of 8 repeating literal
-// n-1 (cap a multiple of 8).  Returns n, the include count.  Wave-uniform.
+// list[0, n) when n <= cap (as entries: lists_scaled), the entries from n to the next
+// multiple of 8 repeating literal n-1 (cap a multiple of 8).  Returns n, the include count.
+// Wave-uniform.
 __device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* list, int cap) {
   // 64 words at a time, one per lane: lane w writes its word's included literals from its
   // prefix-sum offset, lowest bit first, so the list is in increasing literal order
   const int lane = lane_id();
+  const uint32_t scale = lists_scaled(g) ? 4u * (uint32_t)((g.P + 31) / 32) : 1u;
   int total = 0, last = 0;
   for (int64_t wb = 0; wb < g.W; wb += kWave) {
     const int64_t w = wb + lane;
@@ -204,7 +245,7 @@ __device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* li
     int pos = total + incl - pc;
     while (mv) {
       const int b = __ffs((int)mv) - 1;
-      if (pos < cap) list[pos] = (uint16_t)(32 * w + b);
+      if (pos < cap) list[pos] = (uint16_t)((uint32_t)(32 * w + b) * scale);
       ++pos;
       mv &= mv - 1u;
     }
@@ -212,7 +253,7 @@ __device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* li
   }
   if (total > 0 && total <= cap) {
     const int pad_end = ((total + 7) & ~7) < cap ? ((total + 7) & ~7) : cap;
-    for (int p = total + lane; p < pad_end; p += kWave) list[p] = (uint16_t)last;
+    for (int p = total + lane; p < pad_end; p += kWave) list[p] = (uint16_t)((uint32_t)last * scale);
   }
   return total;
 }
@@ -246,13 +287,7 @@ __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16
         const uint2 q0 = *(const uint2*)(list + j), q1 = *(const uint2*)(list + j + 4);
         const uint2 q2 = *(const uint2*)(list + j1), q3 = *(const uint2*)(list + j1 + 4);
         const uint32_t w8[8] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
-        uint32_t v = 0xFFFFFFFFu;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)w];
-          v &= xt[(w8[u] >> 16) * (uint32_t)PW + (uint32_t)w];
-        }
-        part &= v;
+        part &= and_listed(g, w8, xt, (uint32_t)w);
       }
       const unsigned long long live = __ballot(part != 0u);
       bool dead = false;
@@ -274,13 +309,7 @@ __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16
     const uint2 q0 = *(const uint2*)(list + j), q1 = *(const uint2*)(list + j + 4);
     const uint2 q2 = *(const uint2*)(list + j1), q3 = *(const uint2*)(list + j1 + 4);
     const uint32_t w8[8] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
-    uint32_t v = 0xFFFFFFFFu;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + (uint32_t)jl];
-      v &= xt[(w8[u] >> 16) * (uint32_t)PW + (uint32_t)jl];
-    }
-    acc &= v;
+    acc &= and_listed(g, w8, xt, (uint32_t)jl);
     if (!__any(acc != 0u)) break;  // every 16 literals: stop once nothing fires
   }
   return acc;
@@ -394,13 +423,7 @@ __device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const flo
       const uint2 q0 = *(const uint2*)(list + s0), q1 = *(const uint2*)(list + s0 + 4);
       const uint2 q2 = *(const uint2*)(list + s1), q3 = *(const uint2*)(list + s1 + 4);
       const uint32_t w8[8] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
-      uint32_t v = 0xFFFFFFFFu;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        v &= xt[(w8[u] & 0xFFFFu) * (uint32_t)PW + jl];
-        v &= xt[(w8[u] >> 16) * (uint32_t)PW + jl];
-      }
-      acc &= v;
+      acc &= and_listed(g, w8, xt, jl);
     }
     if (!__any(acc != 0u)) break;  // stop once nothing fires anywhere
   }
