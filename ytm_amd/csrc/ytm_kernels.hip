@@ -362,8 +362,9 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
   const int PW = (int)((g.P + 31) / 32);
   const int NG = kWave / PW;
   if (NG >= 2) {
-    const int q = lane / PW, w = lane - q * PW;
-    const bool in_group = q < NG;
+    const int GS = NG == 2 ? 32 : PW;  // two groups: one per 32-lane half
+    const int q = lane / GS, w = lane - q * GS;
+    const bool in_group = q < NG && w < PW;
     uint32_t part = in_group ? (w == PW - 1 && (g.P & 31) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu) : 0u;
     const unsigned long long gmask = (1ull << PW) - 1ull;
     const int nruns = (n + 7) / 8;
@@ -377,7 +378,7 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
       if (in_group && run < nruns) part &= and_listed_as<SCALED>(g, e, xt, (uint32_t)w);
       const unsigned long long live = __ballot(part != 0u);
       bool dead = false;
-      for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * PW)) & gmask) == 0ull;
+      for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * GS)) & gmask) == 0ull;
       if (dead) {
         part = 0u;
         break;
@@ -385,7 +386,7 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
     }
     uint32_t r = part;
     for (int gq = 1; gq < NG; ++gq)
-      r &= (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (w + gq * PW < kWave ? w + gq * PW : lane), (int)part);
+      r &= (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (w + gq * GS < kWave ? w + gq * GS : lane), (int)part);
     return lane < PW ? (r & acc) : 0u;
   }
   const int jl = lane < PW ? lane : 0;

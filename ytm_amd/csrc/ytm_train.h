@@ -270,11 +270,13 @@ __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16
   const int PW = (int)((g.P + 31) / 32);
   const int NG = kWave / PW;  // lane groups of PW lanes
   if (NG >= 2) {
-    // Group q (lanes [q*PW, (q+1)*PW)) ANDs the literal runs 16q, 16q + 16*NG, ... into its own
-    // partial bitmap (lane q*PW + w: word w); a group whose partial is empty everywhere ends
-    // the walk, and the groups' partials are AND-ed together at the end.
-    const int q = lane / PW, w = lane - q * PW;
-    const bool in_group = q < NG;
+    // Group q (lanes [q*GS, q*GS + PW)) ANDs the literal runs 16q, 16q + 16*NG, ... into its
+    // own partial bitmap (lane q*GS + w: word w); a group whose partial is empty everywhere
+    // ends the walk, and the groups' partials are AND-ed together at the end.  Two groups
+    // sit in the two 32-lane halves, so that each half's reads come from one literal's row.
+    const int GS = NG == 2 ? 32 : PW;
+    const int q = lane / GS, w = lane - q * GS;
+    const bool in_group = q < NG && w < PW;
     // word w of the all-patches mask
     uint32_t part = in_group ? (w == PW - 1 && (g.P & 31) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu) : 0u;
     const unsigned long long gmask = PW >= 64 ? ~0ull : ((1ull << PW) - 1ull);
@@ -291,7 +293,7 @@ __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16
       }
       const unsigned long long live = __ballot(part != 0u);
       bool dead = false;
-      for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * PW)) & gmask) == 0ull;
+      for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * GS)) & gmask) == 0ull;
       if (dead) {
         part = 0u;
         break;
@@ -300,7 +302,7 @@ __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16
     // AND of the groups' partials: lane w (< PW) gathers word w of every group
     uint32_t r = part;
     for (int gq = 1; gq < NG; ++gq)
-      r &= (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (w + gq * PW < kWave ? w + gq * PW : lane), (int)part);
+      r &= (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (w + gq * GS < kWave ? w + gq * GS : lane), (int)part);
     return lane < PW ? (r & acc) : 0u;
   }
   const int jl = lane < PW ? lane : 0;
