@@ -68,6 +68,20 @@ def load_traffic(config: int):
         return None
 
 
+def load_counters(config: int):
+    """SQ counters of the training kernel (rocprofv3 --pmc, committed summary): VALU busy,
+    instructions per sample, LDS bank conflicts; or None."""
+    path = ROOT / "profiles" / f"train_cfg{config}_counters.json"
+    if not path.exists():
+        return None
+    try:
+        d = json.loads(path.read_text())
+        return {k: d[k] for k in ("kernel", "valu_busy", "valu_insts_per_sample", "salu_per_valu",
+                                  "lds_bank_conflict", "wait_frac")}
+    except (KeyError, ValueError):
+        return None
+
+
 def cpu_info() -> dict:
     model = platform.processor() or "unknown"
     try:
@@ -289,6 +303,10 @@ def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=No
             # peak the kernel really uses (the byte model above counts reads it never makes)
             res["roofline"]["traffic_gbs"] = traffic["hbm_gbs"]
             res["roofline"]["traffic_frac"] = round(traffic["hbm_gbs"] / HBM_PEAK_GBS, 4)
+    counters = load_counters(cfg)
+    if counters:
+        # measured instruction mix of the same kernel (epoch 2): how busy its execution units are
+        res["binding"]["counters"] = counters
     tm.release()
     if cpu_seconds > 0:
         res["cpu_baseline"] = cpu_baseline(cfg, kw, encX, y, encXt, cpu_seconds)
