@@ -133,3 +133,18 @@ def test_q_is_min_of_q_and_classes():
     # base.py:81 turns an int q >= K into float(K) (a double literal).
     assert min(12, float(10)) == 10.0 and isinstance(min(12, float(10)), float)
     assert isinstance(min(3, float(10)), int)
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_bench_reads_committed_measurements(cfg):
+    """bench.py attaches the committed rocprofv3 measurements of each configuration's
+    training kernel (HBM traffic, SQ counters) to its JSON line: the summaries parse, name
+    the kernel the configuration trains with, and hold consistent figures."""
+    import bench
+    tr = bench.load_traffic(cfg)
+    ct = bench.load_counters(cfg)
+    assert tr is not None and ct is not None
+    assert tr["kernel"].startswith("ytm_jit_train_") and tr["kernel"] == ct["kernel"]
+    assert tr["bytes_per_launch"] > 0 and tr["hbm_gbs"] is not None and 0 < tr["hbm_gbs"] < bench.HBM_PEAK_GBS
+    assert 0.0 <= ct["valu_busy"] <= 1.0 and 0.0 <= ct["lds_bank_conflict"] <= 1.0
+    assert ct["valu_insts_per_sample"] > 0
