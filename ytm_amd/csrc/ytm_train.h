@@ -156,6 +156,7 @@ __device__ __forceinline__ int select_from_bitmap(const TrainArgs& a, const Geom
                                                   uint32_t acc, const float* inv_rank) {
   const int lane = lane_id();
   const int PW = (int)((g.P + 31) / 32);
+  if (!__any(lane < PW && acc != 0u)) return -1;  // no patch fires (most clauses): no scan
   const int pc = lane < PW ? __popc(acc) : 0;
   const int incl = wave_inclusive_scan(pc);
   const int R = lane_value(incl, kWave - 1);
@@ -429,6 +430,7 @@ __device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const flo
     }
     if (!__any(acc != 0u)) break;  // stop once nothing fires anywhere
   }
+  if (!__any(acc != 0u)) return -1;  // no group's clause fires anywhere: no scan
   const int pc = __popc(acc);
   const int incl = group_scan_add<S>(pc);
   const int R = lane_from(incl, gbase + S - 1);  // firing patches of the group's clause
