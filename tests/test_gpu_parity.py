@@ -456,6 +456,25 @@ def test_clause_drop():
     assert_state_equal(tm, ref)
 
 
+@pytest.mark.parametrize("cfg,n,clauses,global_state", [(3, 120, 100, False), (3, 60, 100, True), (4, 12, 60, False)])
+def test_clause_drop_several_patches(monkeypatch, cfg, n, clauses, global_state):
+    """A clause drop mask on models with several patches (resident and global kernels): a
+    dropped clause fires on no patch, so its reservoir step takes the no-firing exit, and
+    neither votes nor learns."""
+    if global_state:
+        monkeypatch.setenv("YTM_TRAIN_GLOBAL", "1")
+    tm, ref, X, y, *_ = pair(cfg, n, clauses=clauses)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    drop_rng = np.random.default_rng(workloads.MODEL_SEED)  # the model's numpy rng (base.py:123,289)
+    for epoch in range(2):
+        tm.fit(encX, y, is_X_encoded=True, clause_drop_p=0.3)
+        drop = (drop_rng.random(ref.C) <= 0.3).astype(np.uint32)
+        upd = ref.fit_encoded(encX, encY, drop=drop)
+        assert tm.stats()["last_fit_updates"] == upd, f"update count epoch {epoch}"
+        assert_state_equal(tm, ref, f"clause drop, epoch {epoch}")
+
+
 def test_launch_shape_independence(monkeypatch):
     """The same seed gives the same model whatever the persistent grid / copy grouping."""
     states = []
