@@ -98,8 +98,9 @@ def test_fit_global_state_kernel(monkeypatch, cfg, n, clauses):
 
 @pytest.mark.parametrize("cfg,n,clauses,global_state,inject",
                          [(1, 2000, None, False, False), (1, 1000, None, True, False), (2, 150, None, False, False),
-                          (2, 100, None, True, False), (3, 40, 100, False, False), (5, 30, 200, False, False),
-                          (1, 40, None, False, True), (3, 4, 12, False, True)])
+                          (2, 100, None, True, False), (3, 40, 100, False, False), (3, 30, 100, True, False),
+                          (4, 6, 60, False, False), (5, 30, 200, False, False), (1, 40, None, False, True),
+                          (3, 4, 12, False, True)])
 def test_fit_builtin_kernels(monkeypatch, cfg, n, clauses, global_state, inject):
     """The built-in training kernels (geometry read from the kernel arguments) give the
     same results as the per-model compiled ones: both against the oracle."""
