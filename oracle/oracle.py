@@ -64,7 +64,7 @@ def load() -> ctypes.CDLL:
             "orc_score": (None, [ctypes.POINTER(OrcParams), _P, _P, _P, _P, ctypes.c_int64, _P]),
             "orc_transform": (None, [ctypes.POINTER(OrcParams), _P, _P, ctypes.c_int64, ctypes.c_int, _P]),
             "orc_fit": (None, [ctypes.POINTER(OrcParams), _P, _P, _P, _P, _P, _P, ctypes.c_int64, _P,
-                               ctypes.c_uint64, _P, _P]),
+                               ctypes.c_uint64, _P, _P, _P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -160,6 +160,15 @@ class OracleTM:
         self.pw = np.zeros((C, self.P), dtype=np.int32)
         self.bias = np.zeros(K, dtype=np.float32)
         self.updates = 0
+        self.last_feedback_samples = 0
+
+    def load_state(self, ta, w, pw, step: int) -> None:
+        """Continue from another model's state: TA states (C, L), weights (C, K), patch
+        weights (C, P) and the step of the random stream (samples trained so far)."""
+        self.ta[...] = np.asarray(ta, dtype=np.uint32).reshape(self.ta.shape)
+        self.w[...] = np.asarray(w, dtype=np.float32).reshape(self.w.shape)
+        self.pw[...] = np.asarray(pw, dtype=np.int32).reshape(self.pw.shape)
+        self.step = int(step)
 
     def encode(self, X: np.ndarray) -> np.ndarray:
         X = np.ascontiguousarray(X, dtype=np.uint32)
@@ -177,11 +186,14 @@ class OracleTM:
             inject = np.ascontiguousarray(inject, dtype=np.float32)
             assert inject.size == N * (self.C * self.P + 2 * self.C * self.K + self.C * self.K * self.L)
         upd = np.zeros(1, dtype=np.uint64)
+        fb = np.zeros(1, dtype=np.uint64)
         self.lib.orc_fit(ctypes.byref(self.p), _addr(self.ta), _addr(self.w), _addr(self.pw), _addr(self.bias),
                          _addr(encX), _addr(encY), N, _addr(drop), ctypes.c_uint64(self.step), _addr(inject),
-                         _addr(upd))
+                         _addr(upd), _addr(fb))
         self.step += N
         self.updates += int(upd[0])
+        # samples of this call at which some class had an update probability above zero
+        self.last_feedback_samples = int(fb[0])
         return int(upd[0])
 
     def encode_y_multiclass(self, Y: np.ndarray) -> np.ndarray:

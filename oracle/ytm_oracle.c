@@ -375,11 +375,14 @@ static void type2_fb(const geom *g, uint32_t *ta, const uint32_t *patch) {
  * sums start from (base.py:327).  drop is the clause drop mask (base.py:288-293).
  * step0 is the model's global step before this call.  inject is NULL (counter stream) or
  * N sample blocks of the injected layout.  *updated_out accumulates the number of
- * (sample, clause) pairs that executed a Type Ia, Ib or II branch.
+ * (sample, clause) pairs that executed a Type Ia, Ib or II branch; *feedback_out (when
+ * not NULL) the samples at which some class has an update probability above zero
+ * (kernel.cu:508-529): only those can change a weight or a TA state, since every update
+ * needs its draw u in (0, 1] at or below that probability (kernel.cu:573-575).
  */
 void orc_fit(const orc_params *p, uint32_t *ta, float *w, int32_t *pw, const float *bias,
              const uint32_t *X, const int32_t *Y, int64_t N, const uint32_t *drop,
-             uint64_t step0, const float *inject, uint64_t *updated_out) {
+             uint64_t step0, const float *inject, uint64_t *updated_out, uint64_t *feedback_out) {
     geom g = geometry(p);
     const int64_t C = g.C, K = g.K, W = g.W, P = g.P, L = g.L;
     const int64_t per_bank = C / (p->coalesced ? 1 : K);
@@ -391,7 +394,7 @@ void orc_fit(const orc_params *p, uint32_t *ta, float *w, int32_t *pw, const flo
     float *clipped = (float *)malloc((size_t)K * sizeof(float));
     int *target = (int *)malloc((size_t)K * sizeof(int));
     double *prob = (double *)malloc((size_t)K * sizeof(double));
-    uint64_t updated = 0;
+    uint64_t updated = 0, feedback = 0;
     const float T = (float)p->thresh;
 
     for (int64_t e = 0; e < N; ++e) {
@@ -448,6 +451,9 @@ void orc_fit(const orc_params *p, uint32_t *ta, float *w, int32_t *pw, const flo
             target[k] = 1 - 2 * (v > (float)y[k]);                    /* :546,571 */
             prob[k] = ((double)y[k] - (double)v) / (2 * (double)y[k]); /* :508-529 */
         }
+        for (int64_t k = 0; k < K; ++k) {
+            if (prob[k] > 0.0) { feedback++; break; }
+        }
         uint64_t upd_count = 0;
 #pragma omp parallel for num_threads(n_threads) schedule(dynamic, 4) reduction(+ : upd_count)
         for (int64_t c = 0; c < C; ++c) {
@@ -488,5 +494,6 @@ void orc_fit(const orc_params *p, uint32_t *ta, float *w, int32_t *pw, const flo
         updated += upd_count;
     }
     if (updated_out) *updated_out += updated;
+    if (feedback_out) *feedback_out += feedback;
     free(masks); free(ninc); free(sel); free(cs_int); free(clipped); free(target); free(prob);
 }

@@ -248,3 +248,107 @@ def test_state_bounds_invariant(oracle_mod):
         assert np.abs(tm.w - w0).max() <= 1
     assert tm.ta.max() <= max(256, 128 + 4)
     assert np.all(tm.w == np.round(tm.w))
+
+
+def test_clause_banks(oracle_mod):
+    """coalesced=False: clause c votes for and learns only its bank's class c // per_bank
+    (kernel.cu:306-312 in select_active, :563-565 in clause_update); inference still sums
+    every class's weight of a firing clause (kernel.cu:337-339); the initial weights are
+    +1 / -1 in the first / second half of the own bank and 0 elsewhere (kernel.cu:58-66)."""
+    # 2 clauses per bank, 2 classes -> C = 4; dim (2,1,1): L = 4 (x0, x1, not x0, not x1).
+    tm = oracle_mod.OracleTM(2, 4, 2.0, (2, 1, 1), 2, coalesced=False)
+    assert tm.C == 4
+    np.testing.assert_array_equal(tm.w, [[1, 0], [-1, 0], [0, 1], [0, -1]])
+    tm.ta[:] = 128
+    tm.ta[0, 0] = 200  # clause 0 (bank 0): x0
+    tm.ta[1, 2] = 200  # clause 1 (bank 0): not x0
+    tm.ta[2, 0] = 200  # clause 2 (bank 1): x0
+    tm.ta[3, 1] = 200  # clause 3 (bank 1): x1
+    # out-of-bank weights set non-zero, so that a vote or an update outside the bank shows
+    tm.w[:] = np.array([[3, 5], [-1, 0], [-7, 2], [0, -1]], dtype=np.float32)
+    enc = tm.encode(np.array([[1, 0]], dtype=np.uint32))  # literals 1, 0, 0, 1
+    Y = np.array([[4, -4]], dtype=np.int32)
+    inj = Inj(tm, fill=0.0)  # every unset draw would take any branch it is asked for
+    for c in range(4):
+        inj.sel(c, 1, 0.5)
+    # clauses 0 and 2 fire.  Class sums over the own bank only: class 0 = w[0,0] = 3,
+    # class 1 = w[2,1] = 2 (not 3 - 7 and 5 + 2).
+    # class 0: v = 3 <= 4 -> target +1, prob (4 - 3) / 8 = 0.125;
+    # class 1: v = 2 > -4 -> target -1, prob (-4 - 2) / -8 = 0.75; Q_PROB = 1.0 (K = 2).
+    inj.upd(0, 0, 0.125)          # clause 0, class 0: u <= prob; sign +1, fires -> Type Ia
+    inj.lit(0, 0, 1, 0.5)         #   0-literal x1: 128 -> 127 (u <= S_INV 0.5)
+    inj.lit(0, 0, 2, 0.75)        #   0-literal not x0: kept
+    inj.upd(1, 0, 0.1)            # clause 1, class 0: sign -1, target +1, not firing -> no branch
+    inj.q(2, 1, 0.9)              # clause 2, class 1: not skipped (0.9 <= 1.0)
+    inj.upd(2, 1, 0.75)           #   u <= 0.75; sign +1, target -1, fires -> Type II
+    inj.q(3, 1, 1.0)              # clause 3, class 1: not skipped (1.0 is not > 1.0)
+    inj.upd(3, 1, 0.7)            #   sign -1, target -1, not firing -> Type Ib
+    inj.lit(3, 1, 0, 0.5)         #   128 -> 127
+    inj.lit(3, 1, 1, 0.6)         #   200 kept
+    inj.lit(3, 1, 2, 0.1)         #   128 -> 127
+    inj.lit(3, 1, 3, 0.7)         #   128 kept
+    upd = tm.fit_encoded(enc, Y, inject=inj.a)
+    assert upd == 3 and tm.last_feedback_samples == 1
+    np.testing.assert_array_equal(tm.ta[0], [201, 127, 128, 129])  # Ia: 1-literals +1
+    np.testing.assert_array_equal(tm.ta[1], [128, 128, 200, 128])
+    np.testing.assert_array_equal(tm.ta[2], [200, 129, 129, 128])  # II: 0-literals +1
+    np.testing.assert_array_equal(tm.ta[3], [127, 200, 127, 128])
+    np.testing.assert_array_equal(tm.w, [[4, 5], [-1, 0], [-7, 1], [0, -1]])
+    np.testing.assert_array_equal(tm.pw, [[1], [0], [1], [0]])
+    # inference: every class sums a firing non-empty clause's weights (kernel.cu:337-339).
+    # The clauses are now 0: x0 AND not x1 (state 129 > 128), 1: not x0, 2: x0 AND x1 AND
+    # not x0 (never fires), 3: x1.  (1, 0) fires clause 0 only, and its out-of-bank weight
+    # 5 counts for class 1; (0, 1) fires clauses 1 and 3; (0, 0) fires clause 1.
+    enc2 = tm.encode(np.array([[1, 0], [0, 1], [0, 0]], dtype=np.uint32))
+    np.testing.assert_array_equal(tm.score(enc2), [[4, 5], [-1 + 0, 0 - 1], [-1, 0]])
+
+
+def test_max_included_literals(oracle_mod):
+    """A firing clause with more included literals than MAX_INCLUDED_LITERALS takes Type Ib
+    instead of Type Ia (kernel.cu:583-586); at the limit it still takes Type Ia."""
+    tm = oracle_mod.OracleTM(2, 4, 2.0, (3, 1, 1), 2, max_included_literals=1, init_neg_weights=False)
+    assert tm.C == 2 and tm.L == 6
+    tm.ta[:] = 128
+    tm.ta[0, [0, 1]] = 150   # clause 0: x0 AND x1 (2 includes > 1)
+    tm.ta[1, 0] = 150        # clause 1: x0 (1 include, at the limit)
+    tm.w[:] = 1.0
+    enc = tm.encode(np.array([[1, 1, 0]], dtype=np.uint32))  # literals 1,1,0 | 0,0,1
+    Y = np.array([[4, -4]], dtype=np.int32)
+    inj = Inj(tm, fill=0.75)
+    inj.sel(0, 1, 0.5)
+    inj.sel(1, 1, 0.5)
+    # class sums 2 and 2.  Class 0: target +1, prob (4 - 2) / 8 = 0.25.
+    # Class 1: target -1, prob (-4 - 2) / -8 = 0.75; u = 0.75 > 0.25 in class 0 by default.
+    inj.upd(0, 0, 0.25)
+    inj.upd(1, 0, 0.25)
+    inj.q(0, 1, 0.5)
+    inj.q(1, 1, 0.5)
+    inj.upd(0, 1, 0.9)       # class 1: no update for either clause
+    inj.upd(1, 1, 0.9)
+    for l in range(6):       # literal draws: decrement exactly literals 0, 2, 4
+        inj.lit(0, 0, l, 0.5 if l % 2 == 0 else 0.6)
+        inj.lit(1, 0, l, 0.5 if l % 2 == 0 else 0.6)
+    upd = tm.fit_encoded(enc, Y, inject=inj.a)
+    assert upd == 2
+    # clause 0, Type Ib: every literal with u <= 0.5 and state > 0 decrements; no weight change
+    np.testing.assert_array_equal(tm.ta[0], [149, 150, 127, 128, 127, 128])
+    # clause 1, Type Ia: 1-literals (0, 1, 5) +1; 0-literals (2, 3, 4) -1 when u <= 0.5
+    np.testing.assert_array_equal(tm.ta[1], [151, 129, 127, 128, 127, 129])
+    np.testing.assert_array_equal(tm.w, [[1, 1], [2, 1]])
+
+
+def test_feedback_sample_count(oracle_mod):
+    """A sample counts as a feedback sample when some class's update probability is above
+    zero: clipped sums at +T for the true class and -T for the others give none."""
+    tm = oracle_mod.OracleTM(1, 1, 2.0, (2, 1, 1), 2, init_neg_weights=False)  # w = [1, 1]
+    tm.w[0] = [1.0, -1.0]
+    enc = tm.encode(np.array([[1, 0]] * 3, dtype=np.uint32))  # the empty clause fires
+    inj = np.full(3 * (tm.C * tm.P + 2 * tm.C * tm.K + tm.C * tm.K * tm.L), 0.5, dtype=np.float32)
+    # class sums (1, -1) with T = 1: at the targets (1, -1) -> no feedback; targets (-1, 1)
+    # -> both classes have probability 1; (1, 1) -> class 1 has probability 1
+    Y = np.array([[1, -1], [-1, 1], [1, 1]], dtype=np.int32)
+    # the first sample changes nothing, so the later ones see the same sums
+    tm.fit_encoded(enc[:1], Y[:1], inject=inj[:inj.size // 3])
+    assert tm.last_feedback_samples == 0
+    tm.fit_encoded(enc[1:2], Y[1:2], inject=np.full(inj.size // 3, 1.0, dtype=np.float32))
+    assert tm.last_feedback_samples == 1
