@@ -117,6 +117,14 @@ typedef struct ytm_stats {
 /* Thread-local description of the last failure. */
 const char *ytm_last_error(void);
 
+/* Unloads the training-kernel modules compiled at run time (each on its device, after a
+ * device synchronize), so that nothing of the library is left on a GPU when the process
+ * exits; call it after destroying every model and dataset.  A later fit loads what it needs
+ * again.  Replaces the context teardown that `import pycuda.autoinit` registers for process
+ * exit (src/cutm/base.py:5), which releases the modules SourceModule loaded
+ * (src/cutm/base.py:155-159).  YTM_EHIP when a module fails to unload. */
+int ytm_shutdown(void);
+
 /* Model lifetime.  Replaces BaseTM._gpu_init / _reset_clauses / _reset_weights
  * (src/cutm/base.py:128-222; kernel.cu:46-73 init_weights): TA states start at
  * number_of_ta_states/2, weights from the INIT random site, patch weights and bias 0. */

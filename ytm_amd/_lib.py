@@ -68,6 +68,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 SIGNATURES = {
     "ytm_last_error": (ctypes.c_char_p, []),
+    "ytm_shutdown": (ctypes.c_int, []),
     "ytm_create": (ctypes.c_int, [ctypes.POINTER(YtmParams), ctypes.POINTER(_P)]),
     "ytm_destroy": (None, [_P]),
     "ytm_geometry": (ctypes.c_int, [_P, _P]),

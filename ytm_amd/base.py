@@ -18,8 +18,10 @@ seed, or from an injected buffer passed as ``fit(..., random_stream=...)``.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import sys
+import weakref
 from typing import Any
 
 import numpy as np
@@ -67,6 +69,34 @@ def typed_q_prob(q: Any, n_classes: int) -> float:
     return (1.0 * float(str(q))) / d
 
 
+# Live models and datasets, released in that order (datasets first) by shutdown().
+_live_data: "weakref.WeakSet[DeviceData]" = weakref.WeakSet()
+_live_models: "weakref.WeakSet[BaseTM]" = weakref.WeakSet()
+
+
+def shutdown() -> None:
+    """Frees every live dataset and model (they are unusable afterwards), then unloads the
+    training kernels compiled at run time (ytm_shutdown).  Registered with atexit, so the
+    device memory, streams, events, pinned buffers and kernel modules of the library are
+    all released while the interpreter and the HIP runtime are still whole, not left to the
+    runtime's own exit handlers."""
+    for d in list(_live_data):
+        d.release()
+    for m in list(_live_models):
+        m.release()
+    check(lib.ytm_shutdown())
+
+
+def _shutdown_at_exit() -> None:
+    try:
+        shutdown()
+    except Exception as exc:  # an exit handler must not raise; report and go on
+        print(f"ytm_amd: teardown at exit failed: {exc}", file=sys.stderr)
+
+
+atexit.register(_shutdown_at_exit)
+
+
 class DeviceData:
     """Encoded samples (and encoded targets) copied once into HBM and owned by libytm."""
 
@@ -76,6 +106,7 @@ class DeviceData:
         handle = ctypes.c_void_p()
         check(lib.ytm_dataset_create(tm._handle, ptr(encoded_X), ptr(encoded_Y), self.n, ctypes.byref(handle)))
         self.handle = handle
+        _live_data.add(self)
 
     def release(self) -> None:
         handle = getattr(self, "handle", None)
@@ -84,8 +115,7 @@ class DeviceData:
         self.handle = None
 
     def __del__(self):
-        # At interpreter exit the HIP runtime may already be torn down; the process
-        # teardown releases the device memory instead.
+        # shutdown() has released everything still alive before the interpreter finalizes
         if not sys.is_finalizing():
             self.release()
 
@@ -221,6 +251,7 @@ class BaseTM:
         handle = ctypes.c_void_p()
         check(lib.ytm_create(ctypes.byref(self._params_c), ctypes.byref(handle)))
         self._handle = handle
+        _live_models.add(self)
 
     def release(self) -> None:
         """Free the model's device memory now (the object is unusable afterwards)."""

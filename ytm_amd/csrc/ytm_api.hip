@@ -417,6 +417,12 @@ extern "C" {
 
 const char* ytm_last_error(void) { return g_error.c_str(); }
 
+int ytm_shutdown(void) {
+  const int failed = ytm::jit_unload_all();
+  if (failed) return fail(YTM_EHIP, std::to_string(failed) + " training-kernel module(s) failed to unload");
+  return YTM_OK;
+}
+
 int ytm_create(const ytm_params* params, ytm_model** out) {
   if (!params || !out) return fail(YTM_EINVAL, "null argument");
   *out = nullptr;
@@ -895,12 +901,18 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu[kMaxDevices];  // held for a whole call: calls on one GPU share the array
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of this device's scratch array (the model's device must be current).
+// Device address of `device`'s scratch array.  The lookup is made with that device current
+// (each device holds its own copy at its own address); the caller's current device is
+// restored afterwards.
 int scratch_address(int device, void** out) {
   if (device < 0 || device >= kMaxDevices) return fail(YTM_EINVAL, "device index out of range for the scratch table");
   if (!g_scratch_ptr[device]) {
+    int prev = -1;
+    hipError_t e = hipGetDevice(&prev);
+    if (e == hipSuccess && prev != device) e = hipSetDevice(device);
     void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
     if (e != hipSuccess || !p)
       return fail(YTM_EHIP, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
     g_scratch_ptr[device] = p;

@@ -96,6 +96,9 @@ int train_rng_slots(int cpw, const Geom& g);
 bool jit_enabled();
 bool jit_compile(const Geom& g, TrainKind kind, bool inject, std::vector<char>* code, std::string* why);
 hipFunction_t jit_train_kernel(const Geom& g, TrainKind kind, bool inject, std::string* why);
+// Unloads every module jit_train_kernel loaded (each on its device, after a device
+// synchronize) and empties the kernel cache; returns the number of modules that failed.
+int jit_unload_all();
 hipError_t jit_occupancy(hipFunction_t fn, int threads, size_t lds_bytes, int* blocks_per_cu);
 hipError_t launch_train_jit(hipFunction_t fn, const TrainArgs& a, int grid, int threads, size_t lds_bytes,
                             hipStream_t s);

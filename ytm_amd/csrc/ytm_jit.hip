@@ -82,10 +82,13 @@ struct Cache {
   std::mutex mu;
   std::map<std::pair<int, std::string>, hipFunction_t> fns;  // (device, source) -> kernel
   std::map<std::string, std::vector<char>> code;              // source -> code object
+  std::vector<std::pair<int, hipModule_t>> modules;           // (device, module) loaded
 };
 
 Cache& cache() {
-  static Cache* c = new Cache();  // never destroyed: modules live until the process ends
+  // never destroyed (no static destructor runs at exit); jit_unload_all() unloads the
+  // modules, which ytm_shutdown() calls before the process ends
+  static Cache* c = new Cache();
   return *c;
 }
 
@@ -186,8 +189,30 @@ hipFunction_t jit_train_kernel(const Geom& g, TrainKind kind, bool inject, std::
     return nullptr;
   }
   std::lock_guard<std::mutex> lk(cache().mu);
-  cache().fns.emplace(std::make_pair(dev, src), fn);
+  auto ins = cache().fns.emplace(std::make_pair(dev, src), fn);
+  if (!ins.second) {  // another thread loaded the same kernel meanwhile: keep one module
+    (void)hipModuleUnload(mod);
+    return ins.first->second;
+  }
+  cache().modules.emplace_back(dev, mod);
   return fn;
+}
+
+int jit_unload_all() {
+  std::lock_guard<std::mutex> lk(cache().mu);
+  if (cache().modules.empty()) return 0;  // no HIP call at all (also on hosts without a GPU)
+  int prev = 0;
+  const bool have_prev = hipGetDevice(&prev) == hipSuccess;
+  int failed = 0;
+  for (const auto& dm : cache().modules) {
+    if (hipSetDevice(dm.first) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipModuleUnload(dm.second) != hipSuccess)
+      ++failed;
+  }
+  cache().modules.clear();
+  cache().fns.clear();
+  if (have_prev) (void)hipSetDevice(prev);
+  return failed;
 }
 
 hipError_t jit_occupancy(hipFunction_t fn, int threads, size_t lds_bytes, int* blocks_per_cu) {
