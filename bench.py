@@ -12,6 +12,7 @@ epochs), each with the C oracle's CPU rate beside it.  Prints ONE JSON line on s
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -30,6 +31,20 @@ VALU_PEAK_T = 256 * 4 * 16 * 2.4e9 / 1e12
 # Epochs of the configurations run after the headline one: (untimed, timed).
 EXTRA_EPOCHS = {1: (1, 10), 2: (1, 3), 3: (1, 2), 4: (1, 2), 5: (1, 2)}
 KIND_NAMES = {0: "resident", 1: "global one-patch", 2: "global several-patch", 3: "streaming"}
+# Training samples of epoch 1 that the CPU baseline trains (None: the whole epoch), fixed so
+# that runs compare; 1000 test samples are scored.
+CPU_PREFIX = {1: None, 2: None, 3: 2000, 4: 1000, 5: 1000}
+# Sources of the training kernels: a committed rocprofv3 summary records their hash, and is
+# reported only while it matches.
+KERNEL_SOURCES = ("ytm_amd/csrc/ytm_train.h", "ytm_amd/csrc/ytm_device.h", "ytm_amd/csrc/ytm_types.h",
+                  "ytm_amd/csrc/ytm_kernels.hip", "ytm_amd/csrc/ytm_api.hip")
+
+
+def kernel_source_hash() -> str:
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES:
+        h.update((ROOT / f).read_bytes())
+    return h.hexdigest()[:16]
 
 
 def log(msg: str) -> None:
@@ -54,32 +69,109 @@ def infer_bytes(tm, samples: int) -> float:
     return float(samples * (4 * tm.number_of_patches * tm.number_of_literal_chunks + 4 * tm.number_of_outputs))
 
 
-def load_traffic(config: int):
-    """HBM bytes per training-kernel launch measured with rocprofv3 --pmc FETCH_SIZE /
-    WRITE_SIZE (committed summary), or None."""
-    path = ROOT / "profiles" / f"train_cfg{config}_traffic.json"
+def load_profile(name: str):
+    """A committed rocprofv3 summary (profiles/<name>.json), or None when it is absent, or
+    measured on kernel sources other than the current ones (its source_sha16 differs)."""
+    path = ROOT / "profiles" / f"{name}.json"
     if not path.exists():
         return None
     try:
         d = json.loads(path.read_text())
-        return {"bytes_per_launch": float(d["bytes_per_launch"]), "kernel": d.get("kernel"),
-                "hbm_gbs": d.get("hbm_gbs")}
+    except ValueError:
+        return None
+    if d.get("source_sha16") != kernel_source_hash():
+        log(f"[bench] profiles/{name}.json was measured on other kernel sources: not reported")
+        return None
+    return d
+
+
+def load_traffic(config: int):
+    """HBM bytes per training-kernel launch measured with rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE (committed summary of the timed epochs), or None."""
+    d = load_profile(f"train_cfg{config}_traffic")
+    try:
+        return None if d is None else {"bytes_per_launch": float(d["bytes_per_launch"]), "kernel": d.get("kernel"),
+                                       "hbm_gbs": d.get("hbm_gbs"), "epochs": d.get("epochs")}
     except (KeyError, ValueError):
         return None
 
 
 def load_counters(config: int):
-    """SQ counters of the training kernel (rocprofv3 --pmc, committed summary): VALU busy,
-    instructions per sample, LDS bank conflicts; or None."""
-    path = ROOT / "profiles" / f"train_cfg{config}_counters.json"
-    if not path.exists():
-        return None
+    """SQ counters of the training kernel (rocprofv3 --pmc, committed summary of the timed
+    epochs): VALU busy, instructions per sample, LDS bank conflicts; or None."""
+    d = load_profile(f"train_cfg{config}_counters")
     try:
-        d = json.loads(path.read_text())
-        return {k: d[k] for k in ("kernel", "valu_busy", "valu_insts_per_sample", "salu_per_valu",
-                                  "lds_bank_conflict", "wait_frac")}
-    except (KeyError, ValueError):
+        return None if d is None else {k: d[k] for k in ("kernel", "epochs", "valu_busy", "valu_insts_per_sample",
+                                                         "salu_per_valu", "lds_bank_conflict", "wait_frac")}
+    except KeyError:
         return None
+
+
+def _load_state(tm, ta, w) -> None:
+    tm.load_state_dict({"state": {"ta_state": ta, "clause_weights": w,
+                                  "patch_weights": np.zeros((tm.number_of_clauses, tm.number_of_patches), np.int32),
+                                  "min_y": None, "max_y": None}})
+
+
+def floor_us(kw: dict, mode: str, n: int):
+    """Microseconds per sample that the training kernel of a model with the geometry (and so
+    the launch shape) of kw takes on a crafted workload of n all-zero samples of class 0, where
+    the kernel does the least it can: the floor its class-sum exchange sets.  Weights are +m
+    for class 0 and -m for the others with m * C >= T, so firing clauses put every class sum
+    at its clip, and no sample needs feedback:
+      "stream": every clause empty (it fires on the one patch), the streaming kernel, which
+          then never stops;
+      "exchange": the resident kernel (one grid-wide exchange per sample).  One patch: empty
+          clauses; several patches: every clause holds the last bit of both position
+          thermometers, so that it fires on the last patch only (one literal list step, one
+          reservoir draw);
+      "stop": the streaming kernel with every clause holding literal 0 (a pixel, 0 in every
+          sample: it never fires) and weights -1 for class 0, +1 for the others: every class
+          sum is 0, every sample needs feedback (probability 1/2), and no branch applies
+          (Type II needs a firing clause; target * sign < 0 everywhere): a stop per sample,
+          without updates.
+    Returns None when the run does not behave as intended (checked from the kernel's
+    counters)."""
+    from ytm_amd import MultiClassTM
+
+    env = {"stream": "1", "stop": "1", "exchange": "0"}[mode]
+    old = os.environ.get("YTM_TRAIN_STREAM")
+    os.environ["YTM_TRAIN_STREAM"] = env
+    try:
+        tm = MultiClassTM(**kw)
+        C, K, L, P = tm.number_of_clauses, tm.number_of_outputs, tm.number_of_literals, tm.number_of_patches
+        half = tm.number_of_ta_states // 2
+        ta = np.full((C, L), half, dtype=np.uint32)
+        m = -(-int(kw["T"]) // C)
+        w = np.full((C, K), -float(m), dtype=np.float32)
+        w[:, 0] = m
+        if mode == "stop":
+            ta[:, 0] = tm.number_of_ta_states
+            w = -w / m
+        elif mode == "exchange" and P > 1:
+            ty, tx = kw["dim"][1] - kw["patch_dim"][1], kw["dim"][0] - kw["patch_dim"][0]
+            ta[:, [ty - 1, ty + tx - 1]] = tm.number_of_ta_states
+        _load_state(tm, ta, w)
+        X = np.zeros((n, kw["dim"][0] * kw["dim"][1] * kw["dim"][2]), dtype=np.uint32)
+        data = tm.device_data(X, np.zeros(n, dtype=np.uint32))
+        tm.fit_device(data)
+        st = tm.stats()
+        data.release()
+        tm.release()
+    finally:
+        if old is None:
+            os.environ.pop("YTM_TRAIN_STREAM", None)
+        else:
+            os.environ["YTM_TRAIN_STREAM"] = old
+    want_kind = 0 if mode == "exchange" else 3
+    want_fb = n if mode == "stop" else 0
+    if st["train_kind"] != want_kind or st["last_fit_feedback_samples"] != want_fb or st["last_fit_updates"] != 0:
+        log(f"[bench] floor run {mode}: kernel {st['train_kind']}, feedback samples {st['last_fit_feedback_samples']}, "
+            f"updates {st['last_fit_updates']}: not the intended workload, left out")
+        return None
+    us = 1e3 * st["last_fit_kernel_ms"] / n
+    log(f"[bench] floor run {mode}: {n} samples, {us:.3f} us/sample, {st['train_workgroups']} workgroups")
+    return us
 
 
 def cpu_info() -> dict:
@@ -127,10 +219,11 @@ def encode_in_chunks(tm, make_chunk, n: int, chunk: int) -> np.ndarray:
     return out
 
 
-def cpu_baseline(cfg: int, kw: dict, encX, y, encXt, budget_s: float) -> dict:
+def cpu_baseline(cfg: int, kw: dict, encX, y, encXt, n_train: int | None) -> dict:
     """The C oracle (a CPU restatement of the reference semantics, oracle/ytm_oracle.c)
-    training on a prefix of the same workload from the same initial state, then scoring a
-    prefix of the test set, on this host's cores (OpenMP)."""
+    training on the first n_train samples of epoch 1 of the same workload (all of them when
+    None) from the same initial state, then scoring 1000 test samples, on this host's cores
+    (OpenMP)."""
     from oracle import oracle as orc
 
     info = cpu_info()
@@ -138,16 +231,10 @@ def cpu_baseline(cfg: int, kw: dict, encX, y, encXt, budget_s: float) -> dict:
     orc.set_threads(threads)
     ref = orc.OracleTM(kw["number_of_clauses_per_class"], kw["T"], kw["s"], kw["dim"], kw["n_classes"],
                        patch_dim=kw.get("patch_dim"), seed=kw["seed"])
-    encY = ref.encode_y_multiclass(y)
-    # consecutive chunks of epoch 1 (the oracle's step counter carries across calls, so this
-    # is the same computation as one fit over the prefix) until the budget is spent
+    n = encX.shape[0] if n_train is None else min(n_train, encX.shape[0])
+    encY = ref.encode_y_multiclass(y[:n])
     t0 = time.perf_counter()
-    n, chunk = 0, 8
-    while n < encX.shape[0] and time.perf_counter() - t0 < budget_s:
-        m = min(chunk, encX.shape[0] - n)
-        ref.fit_encoded(encX[n:n + m], encY[n:n + m])
-        n += m
-        chunk = min(2 * chunk, 2048)
+    ref.fit_encoded(encX[:n], encY)
     train_s = time.perf_counter() - t0
     nt = min(encXt.shape[0], 1000)
     t1 = time.perf_counter()
@@ -167,7 +254,8 @@ def cpu_baseline(cfg: int, kw: dict, encX, y, encXt, budget_s: float) -> dict:
     }
 
 
-def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=None, n_test=None) -> dict:
+def run_config(cfg: int, warmup: int, steps: int, cpu: bool, n_train=None, n_test=None, cpu_samples=None,
+               floors: bool = True) -> dict:
     import workloads
     from ytm_amd import MultiClassTM
 
@@ -276,6 +364,10 @@ def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=No
             "traffic": None,
             "U_s": round(upd / (N * steps), 3),
             "bytes_per_launch": round(byts / max(1, launches), 1),
+            "model": "algorithmic bytes (N*C + U)(2L + 4K) + 4NPW per launch: every TA state read at 2 B and "
+                     "every weight at 4 B per sample, updated clauses written back, each sample read once. The "
+                     "kernels keep the clause state on chip and do not make these reads, so a frac above 1 is the "
+                     "on-chip saving, not HBM use; binding.bound is what limits the kernel",
         },
         # what actually binds the training kernel: the share of its time spent waiting for
         # class sums, and how many samples needed a feedback pass
@@ -305,12 +397,65 @@ def run_config(cfg: int, warmup: int, steps: int, cpu_seconds: float, n_train=No
             res["roofline"]["traffic_frac"] = round(traffic["hbm_gbs"] / HBM_PEAK_GBS, 4)
     counters = load_counters(cfg)
     if counters:
-        # measured instruction mix of the same kernel (epoch 2): how busy its execution units are
+        # measured instruction mix of the same kernel (timed epochs): how busy its execution units are
         res["binding"]["counters"] = counters
+    if cfg in (4,):
+        # work model of the list walks from the trained state: each clause ANDs the PW-word
+        # bitsets of its included literals (no early exit), per sample
+        n_inc = tm.get_literals().reshape(tm.number_of_clauses, -1).sum(axis=1, dtype=np.int64)
+        pw_words = (tm.number_of_patches + 31) // 32
+        ands = float(n_inc.sum()) * pw_words
     tm.release()
-    if cpu_seconds > 0:
-        res["cpu_baseline"] = cpu_baseline(cfg, kw, encX, y, encXt, cpu_seconds)
+    res["binding"]["bound"] = bound_of(cfg, kw, res, timed, N, kern_s, traffic, ands if cfg in (4,) else None,
+                                       floors)
+    if cpu:
+        res["cpu_baseline"] = cpu_baseline(cfg, kw, encX, y, encXt,
+                                           cpu_samples if cpu_samples is not None else CPU_PREFIX[cfg])
     return res
+
+
+def bound_of(cfg: int, kw: dict, res: dict, timed: list, N: int, kern_s: float, traffic, list_ands, floors: bool):
+    """What bounds the training kernel in the timed epochs, as {resource, achieved, peak,
+    frac} with frac = achieved / peak <= 1, each figure measured in this run or read from a
+    committed profile of the current kernel sources:
+      configs 1 and 3 (resident kernel): one grid-wide class-sum exchange per sample; peak =
+        the samples/s of the same kernel on the same grid when it does nothing but exchange
+        (floor_us "exchange");
+      config 2 (streaming kernel): the class-sum rows; peak = the samples/s of the timed
+        epochs' mix of stops and streamed samples at the kernel's floors (floor_us "stop"
+        for each stop, "stream" for every other sample);
+      config 4: VALU, the list walks' word-ANDs of the trained state (sum of include counts
+        times ceil(P/32) per sample) against 256 CUs x 64 lanes x 2.4 GHz;
+      config 5: HBM, the measured traffic of a timed-epoch launch (rocprofv3 FETCH_SIZE +
+        WRITE_SIZE, calibrated) against 8 TB/s."""
+    steps = len(timed)
+    rate = N * steps / kern_s
+    if cfg in (1, 3) and floors:
+        f = floor_us(kw, "exchange", min(N, 10000))
+        if f is None:
+            return None
+        return {"resource": "class-sum exchange, one per sample (resident kernel)", "unit": "samples/s",
+                "achieved": round(rate, 1), "peak": round(1e6 / f, 1), "frac": round(rate * f / 1e6, 4),
+                "floor_us_per_sample": round(f, 4)}
+    if cfg == 2 and floors:
+        fs, fp = floor_us(kw, "stream", 30000), floor_us(kw, "stop", 30000)
+        if fs is None or fp is None:
+            return None
+        stops = sum(e["feedback"] for e in timed)
+        t_min = ((N * steps - stops) * fs + stops * fp) / 1e6
+        return {"resource": "class-sum rows (streaming kernel): streamed samples and stops", "unit": "samples/s",
+                "achieved": round(rate, 1), "peak": round(N * steps / t_min, 1), "frac": round(t_min / kern_s, 4),
+                "stream_floor_us_per_sample": round(fs, 4), "stop_floor_us": round(fp, 4), "stops": stops}
+    if cfg == 4 and list_ands is not None:
+        ach = list_ands * rate / 1e12
+        return {"resource": "VALU: list-walk word-ANDs of the trained state (include counts x ceil(P/32))",
+                "unit": "T lane-ops/s", "achieved": round(ach, 3), "peak": round(VALU_PEAK_T, 2),
+                "frac": round(ach / VALU_PEAK_T, 4), "word_ands_per_sample": list_ands}
+    if cfg == 5 and traffic and traffic.get("hbm_gbs"):
+        return {"resource": "HBM: measured traffic of a timed-epoch launch", "unit": "GB/s",
+                "achieved": traffic["hbm_gbs"], "peak": HBM_PEAK_GBS,
+                "frac": round(traffic["hbm_gbs"] / HBM_PEAK_GBS, 4), "epochs": traffic.get("epochs")}
+    return None
 
 
 def main() -> int:
@@ -321,8 +466,10 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--n-train", type=int, default=None)
     ap.add_argument("--n-test", type=int, default=None)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-oracle budget per configuration")
+    ap.add_argument("--cpu-samples", type=int, default=None,
+                    help="training samples of the CPU baseline (default: a fixed prefix per configuration)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-floors", action="store_true", help="skip the floor runs behind binding.bound")
     ap.add_argument("--no-extra", action="store_true", help="only the headline configuration")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device (counter calibration under rocprofv3 --pmc)")
@@ -334,15 +481,15 @@ def main() -> int:
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
 
-    cpu = 0.0 if args.no_cpu else args.cpu_seconds
     cfg = args.config
-    head = run_config(cfg, args.warmup, args.steps, cpu, args.n_train, args.n_test)
+    cpu, floors = not args.no_cpu, not args.no_floors
+    head = run_config(cfg, args.warmup, args.steps, cpu, args.n_train, args.n_test, args.cpu_samples, floors)
     configs = {str(cfg): head}
     if not args.no_extra:
         for other in (1, 2, 3, 4, 5):
             if other != cfg:
                 w, s = EXTRA_EPOCHS[other]
-                configs[str(other)] = run_config(other, w, s, cpu)
+                configs[str(other)] = run_config(other, w, s, cpu, cpu_samples=args.cpu_samples, floors=floors)
 
     import workloads
 
@@ -375,6 +522,7 @@ def main() -> int:
         },
         "infer_samples_per_s": head["infer_samples_per_s"],
         "roofline": head["roofline"],
+        "binding": head["binding"],
         "cpu_baseline": head.get("cpu_baseline"),
         "configs": {k: {kk: vv for kk, vv in v.items() if not kk.startswith("_")} for k, v in configs.items()},
     }

@@ -136,15 +136,48 @@ def test_q_is_min_of_q_and_classes():
 
 
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
-def test_bench_reads_committed_measurements(cfg):
-    """bench.py attaches the committed rocprofv3 measurements of each configuration's
-    training kernel (HBM traffic, SQ counters) to its JSON line: the summaries parse, name
-    the kernel the configuration trains with, and hold consistent figures."""
+def test_bench_profile_summaries(cfg):
+    """The committed rocprofv3 summaries of each configuration's training kernel (HBM traffic,
+    SQ counters) parse, name the kernel the configuration trains with, hold consistent
+    figures, and record the hash of the kernel sources they were measured on."""
+    import json
+
     import bench
-    tr = bench.load_traffic(cfg)
-    ct = bench.load_counters(cfg)
-    assert tr is not None and ct is not None
+    tr = json.loads((bench.ROOT / "profiles" / f"train_cfg{cfg}_traffic.json").read_text())
+    ct = json.loads((bench.ROOT / "profiles" / f"train_cfg{cfg}_counters.json").read_text())
     assert tr["kernel"].startswith("ytm_jit_train_") and tr["kernel"] == ct["kernel"]
-    assert tr["bytes_per_launch"] > 0 and tr["hbm_gbs"] is not None and 0 < tr["hbm_gbs"] < bench.HBM_PEAK_GBS
+    assert tr["bytes_per_launch"] > 0 and 0 < tr["hbm_gbs"] < bench.HBM_PEAK_GBS
     assert 0.0 <= ct["valu_busy"] <= 1.0 and 0.0 <= ct["lds_bank_conflict"] <= 1.0
     assert ct["valu_insts_per_sample"] > 0
+    for d in (tr, ct):
+        if "source_sha16" in d:
+            assert len(d["source_sha16"]) == 16 and int(d["source_sha16"], 16) >= 0
+
+
+def test_bench_reports_only_current_profiles(tmp_path, monkeypatch):
+    """A summary measured on other kernel sources (another source_sha16) is not reported."""
+    import json
+
+    import bench
+    (tmp_path / "profiles").mkdir()
+    d = {"kernel": "ytm_jit_train_stream", "bytes_per_launch": 1.0, "hbm_gbs": 1.0}
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    monkeypatch.setattr(bench, "kernel_source_hash", lambda: "0123456789abcdef")
+    (tmp_path / "profiles" / "train_cfg2_traffic.json").write_text(json.dumps(dict(d, source_sha16="fedcba9876543210")))
+    assert bench.load_traffic(2) is None
+    (tmp_path / "profiles" / "train_cfg2_traffic.json").write_text(json.dumps(dict(d, source_sha16="0123456789abcdef")))
+    assert bench.load_traffic(2)["bytes_per_launch"] == 1.0
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_bench_bound_is_a_fraction(cfg, monkeypatch):
+    """binding.bound puts each configuration's measured rate against a peak it cannot pass:
+    with floors below the measured per-sample time, 0 < frac <= 1 and frac = achieved / peak."""
+    import bench
+    N, kern_s = 60000, 0.3  # 5 us per sample
+    timed = [{"feedback": 1000}, {"feedback": 500}]
+    monkeypatch.setattr(bench, "floor_us", lambda kw, mode, n: {"exchange": 2.0, "stream": 0.2, "stop": 4.0}[mode])
+    traffic = {"hbm_gbs": 4000.0, "epochs": [6, 7]}
+    b = bench.bound_of(cfg, {}, {}, timed, N, 2 * kern_s, traffic, 3.0e7, True)
+    assert b is not None and 0.0 < b["frac"] <= 1.0
+    assert abs(b["achieved"] / b["peak"] - b["frac"]) < 1e-3
