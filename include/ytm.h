@@ -159,6 +159,17 @@ int ytm_load_train_kernels(ytm_model *m, int32_t kinds[4], int32_t *n_kinds);
  * X: uint32 (N, dim0*dim1*dim2), any value > 0 is a set pixel.  out: uint32 (N, P, W). */
 int ytm_encode(ytm_model *m, const uint32_t *X, int64_t N, uint32_t *out);
 
+/* encode of binned raw values in one pass, without the binned array: the transform of
+ * Binarizer / ThermometerBinarizer (src/tm_utils/binarizer.py:9-22,63-86) followed by
+ * BaseTM.encode (src/cutm/base.py:224-263; kernel.cu:76-152).  X holds N samples of
+ * dim0*dim1*dim2 / width raw values of type x_dtype (YTM_DTYPE_*); value i of a sample
+ * becomes the width levels (kind 0 thermometer: width = nthr; kind 1 one-hot: width =
+ * nthr - 1 + 2 * edge_bins) at positions [i * width, (i + 1) * width) of the binned row,
+ * as ytm_binarize lays them out, with the same thresholds and comparison types.  out: uint32
+ * (N, P, W), equal to ytm_encode of the binned rows. */
+int ytm_encode_binarized(ytm_model *m, const void *X, int x_dtype, int64_t N, const void *thresholds,
+                         int int_thresholds, int nthr, int kind, int edge_bins, uint32_t *out);
+
 /* Device-resident training / scoring data, so repeated epochs do not re-copy it.
  * encX: uint32 (N, P, W); encY: int32 (N, classes) or NULL for score-only data. */
 int ytm_dataset_create(ytm_model *m, const uint32_t *encX, const int32_t *encY, int64_t N,

@@ -135,3 +135,60 @@ def test_large_transform_properties():
     level = np.searchsorted(ob.thermometer_thresholds(8), rgb, side="right")
     np.testing.assert_array_equal(out.sum(-1, dtype=np.int64), level)
     assert np.all(np.diff(out.astype(np.int8), axis=-1) <= 0)
+
+
+# ------------------------------------------------------------------ binning fused into encode
+@pytest.mark.parametrize("case", ["rgb", "gray", "thermometer", "thermometer_edges", "onehot", "onehot_edges",
+                                  "int_thresholds"])
+def test_encode_binarized(case):
+    """encode_binarized (ytm_encode_binarized: the binning done where encode reads each value)
+    gives the words of encode() on the binarizer's output, and of the oracle's encode of the
+    oracle's binning: ThermometerBinarizer on uint8 images (config 4's CIFAR shape, 3x3
+    patches; a gray config-3 shape, 10x10 patches), and Binarizer thermometer / one-hot codes,
+    with and without edge bins, on a one-patch model, float data and integer data with integer
+    thresholds."""
+    from ytm_amd import MultiClassTM
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(zlib.crc32(case.encode()))
+    if case == "rgb":
+        X = rng.integers(0, 256, (5, 32, 32, 3)).astype(np.uint8)
+        b = ThermometerBinarizer(8)
+        kw = dict(dim=(32, 32, 24), patch_dim=(3, 3))
+        binned = ob.thermometer(X, ob.thermometer_thresholds(8))
+    elif case == "gray":
+        X = rng.integers(0, 256, (4, 28, 28)).astype(np.uint8)
+        b = ThermometerBinarizer(3)
+        kw = dict(dim=(28, 28, 3), patch_dim=(10, 10))
+        binned = ob.thermometer(X, ob.thermometer_thresholds(3))
+    else:
+        edge = case.endswith("edges")
+        kind = "onehot" if case.startswith("onehot") else "thermometer"
+        if case == "int_thresholds":
+            X = rng.integers(-50, 50, (30, 40)).astype(np.int16)
+            b = Binarizer(3, type="thermometer")
+            b.fit(X, thresholds=np.array([-10, 0, 25], dtype=np.int64))
+            t = ob.fit_thresholds(X, 3, thresholds=np.array([-10, 0, 25], dtype=np.int64))
+        else:
+            X = rng.normal(size=(30, 40)).astype(np.float32)
+            b = Binarizer(4, edge_bins=edge, type=kind)
+            b.fit(X)
+            t = ob.fit_thresholds(X, 4)
+        binned = (ob.thermometer(X, t if edge else t[1:-1]) if kind == "thermometer" or case == "int_thresholds"
+                  else ob.onehot(X, t, edge))
+        kw = dict(dim=(40 * binned.shape[-1], 1, 1))
+    N = X.shape[0]
+    tm = MultiClassTM(4, 10, 3.0, n_classes=2, seed=1, **kw)
+    ref = orc.OracleTM(4, 10, 3.0, n_classes=2, seed=1, **kw)
+    got = tm.encode_binarized(X, b)
+    binned = np.ascontiguousarray(binned.reshape(N, -1), dtype=np.uint32)
+    np.testing.assert_array_equal(got, tm.encode(binned), err_msg=f"{case}: against encode of the binned rows")
+    np.testing.assert_array_equal(got, ref.encode(binned), err_msg=f"{case}: against the oracle")
+
+
+def test_encode_binarized_checks_the_size():
+    from ytm_amd import MultiClassTM
+
+    tm = MultiClassTM(4, 10, 3.0, (32, 32, 24), 2, patch_dim=(3, 3), seed=1)
+    with pytest.raises(AssertionError):
+        tm.encode_binarized(np.zeros((2, 32, 32, 3), dtype=np.uint8), ThermometerBinarizer(4))

@@ -62,16 +62,21 @@ def _mnist_shaped(rng, n_train, n_test):
     return X, y, Xt, yt
 
 
+def _cifar_images(rng, means, labels):
+    """uint8 images (n, 32, 32, 3) of the given classes: the class's colour field plus noise."""
+    n = labels.shape[0]
+    return np.clip(means[labels] + rng.normal(0.0, 32.0, (n, 32, 32, 3)), 0, 255).astype(np.uint8)
+
+
 def _cifar_rows(rng, means, labels):
     # thermometer j = 0..7: x >= (j+1)*255/9, layout [y][x][channel*8 + j]
     # (the closed form of src/tm_utils/binarizer.py:11,19)
-    n = labels.shape[0]
+    img = _cifar_images(rng, means, labels)
     thr = (np.arange(1, 9) * 255.0 / 9.0)
-    img = np.clip(means[labels] + rng.normal(0.0, 32.0, (n, 32, 32, 3)), 0, 255).astype(np.uint8)
-    return (img[..., None] >= thr).reshape(n, 32 * 32 * 24).astype(np.uint32)  # (n, 32, 32, 3, 8)
+    return (img[..., None] >= thr).reshape(labels.shape[0], 32 * 32 * 24).astype(np.uint32)  # (n, 32, 32, 3, 8)
 
 
-def _cifar_images(rng, means, n, chunk=1024):
+def _cifar_set(rng, means, n, chunk=1024):
     # The noise is drawn chunk by chunk, which gives the same values as one draw of the whole
     # (n, 32, 32, 3) array while the temporaries stay in cache.
     y = rng.integers(0, means.shape[0], n)
@@ -95,8 +100,8 @@ def _cifar_means(rng):
 
 def _cifar_shaped(rng, n_train, n_test):
     means = _cifar_means(rng)
-    X, y = _cifar_images(rng, means, n_train)
-    Xt, yt = _cifar_images(rng, means, n_test)
+    X, y = _cifar_set(rng, means, n_train)
+    Xt, yt = _cifar_set(rng, means, n_test)
     return X, y, Xt, yt
 
 
@@ -122,13 +127,28 @@ class CifarStream:
         return _cifar_rows(self._rng, self._means, self._y[s:e])
 
     def test_rows(self, s, e):
+        self._start_test(s)
+        self._pos = self.n_train + e
+        return _cifar_rows(self._rng, self._means, self._yt[s:e])
+
+    def train_images(self, s, e):
+        """The uint8 images (e - s, 32, 32, 3) behind train_rows(s, e): their rows are
+        ThermometerBinarizer(8).binarize_rgb of these, flattened."""
+        assert s == self._pos and e <= self.n_train, "rows must be generated in order"
+        self._pos = e
+        return _cifar_images(self._rng, self._means, self._y[s:e])
+
+    def test_images(self, s, e):
+        self._start_test(s)
+        self._pos = self.n_train + e
+        return _cifar_images(self._rng, self._means, self._yt[s:e])
+
+    def _start_test(self, s):
         if self._yt is None:
             assert self._pos == self.n_train, "the training rows come first"
             self._yt = self._rng.integers(0, 10, self.n_test)
             self.yt = self._yt.astype(np.uint32)
-        assert s == self._pos - self.n_train and e <= self.n_test, "rows must be generated in order"
-        self._pos = self.n_train + e
-        return _cifar_rows(self._rng, self._means, self._yt[s:e])
+        assert s == self._pos - self.n_train, "rows must be generated in order"
 
 
 def _docs(rng, probs, n, length=150):

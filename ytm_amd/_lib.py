@@ -77,6 +77,8 @@ SIGNATURES = {
     "ytm_compile_train_kernel": (ctypes.c_int, [ctypes.POINTER(YtmParams), ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "ytm_load_train_kernels": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
     "ytm_encode": (ctypes.c_int, [_P, _P, _I64, _P]),
+    "ytm_encode_binarized": (ctypes.c_int, [_P, _P, ctypes.c_int, _I64, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, _P]),
     "ytm_dataset_create": (ctypes.c_int, [_P, _P, _P, _I64, ctypes.POINTER(_P)]),
     "ytm_dataset_destroy": (None, [_P]),
     "ytm_fit_dataset": (ctypes.c_int, [_P, _P, _I64, _I64, _P, _P]),

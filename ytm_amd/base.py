@@ -284,6 +284,28 @@ class BaseTM:
         check(lib.ytm_encode(self._handle, ptr(X), N, ptr(out)))
         return out
 
+    def encode_binarized(self, X: np.ndarray, binarizer) -> np.ndarray:
+        """encode() of the binarizer's output for X in one pass on the GPU, without the binned
+        array: X holds N samples of raw values (any shape (N, ...)), binned by a
+        ThermometerBinarizer or a fitted Binarizer (src/tm_utils/binarizer.py), whose levels
+        of a value are consecutive in the binned row.  The result equals
+        ``self.encode(binned.reshape(N, -1))`` where binned is binarize_gray / binarize_rgb /
+        transform of X (not in the reference, which bins on the host: 1/width of the input
+        bytes to move, and no binned array)."""
+        from .binarizer import _device_levels, _dtype_code
+
+        thresholds, kind, edge = binarizer._levels()
+        Xd, t, int_thr, width = _device_levels(X, thresholds, kind, edge)
+        assert Xd.ndim >= 2, "X must hold samples along its first axis."
+        N = Xd.shape[0]
+        F = self.dim[0] * self.dim[1] * self.dim[2]
+        assert Xd[0].size * width == F, (
+            f"X's samples bin to {Xd[0].size} x {width} values; the model takes dim0 * dim1 * dim2 = {F}.")
+        out = np.empty((N, self.number_of_patches, self.number_of_literal_chunks), dtype=np.uint32)
+        check(lib.ytm_encode_binarized(self._handle, ptr(Xd), _dtype_code(Xd), N, ptr(t), int(int_thr), t.size,
+                                       kind, int(bool(edge)), ptr(out)))
+        return out
+
     def _check_encoded(self, encoded_X: np.ndarray) -> np.ndarray:
         assert encoded_X.dtype == np.uint32, "encoded X must be of type np.uint32."
         assert encoded_X.shape[1:] == (self.number_of_patches, self.number_of_literal_chunks), (

@@ -21,6 +21,11 @@ from ._lib import DTYPES, check, lib, ptr
 _THERMOMETER, _ONEHOT = 0, 1
 
 
+def _dtype_code(Xd: np.ndarray) -> int:
+    """YTM_DTYPE_* code of an array _device_input returned."""
+    return DTYPES[Xd.dtype.name]
+
+
 def _device_input(X: np.ndarray) -> np.ndarray:
     """X as a contiguous array of a type the GPU kernels take, with the same values."""
     X = np.asarray(X)
@@ -35,14 +40,21 @@ def _device_input(X: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(X)
 
 
-def _binarize(X, thresholds, kind: int, edge_bins: bool) -> np.ndarray:
+def _device_levels(X, thresholds, kind: int, edge_bins: bool):
+    """(X for the kernels, threshold array, whether the comparison is in int64, levels per
+    value) of a binning: the comparison type numpy promotes X and the thresholds to."""
     Xd = _device_input(X)
     t = np.asarray(thresholds)
     int_thr = (np.issubdtype(t.dtype, np.integer) and t.dtype != np.uint64
                and np.issubdtype(Xd.dtype, np.integer))
     t = np.ascontiguousarray(t, dtype=np.int64 if int_thr else np.float64)
+    width = t.size if kind == _THERMOMETER else t.size - 1 + (2 if edge_bins else 0)
+    return Xd, t, int_thr, width
+
+
+def _binarize(X, thresholds, kind: int, edge_bins: bool) -> np.ndarray:
+    Xd, t, int_thr, width = _device_levels(X, thresholds, kind, edge_bins)
     nthr = t.size
-    width = nthr if kind == _THERMOMETER else nthr - 1 + (2 if edge_bins else 0)
     out = np.empty(Xd.shape + (width,), dtype=np.uint32)
     check(lib.ytm_binarize(ptr(Xd), DTYPES[Xd.dtype.name], Xd.size, ptr(t), int(int_thr), nthr, kind,
                            int(bool(edge_bins)), ptr(out)))
@@ -70,6 +82,10 @@ class ThermometerBinarizer:
 
     def _thresholds(self) -> np.ndarray:
         return np.arange(1, self.ch + 1) * 255 / (self.ch + 1)
+
+    def _levels(self):
+        """Thresholds, kind and edge flag of the binning (for encode_binarized)."""
+        return self._thresholds(), _THERMOMETER, False
 
     def binarize_gray(self, X):
         """(N, H, W) -> uint32 (N, H, W, ch)."""
@@ -115,6 +131,14 @@ class Binarizer:
             raise ValueError(f"Unknown method: {self.method}")
         self.thresholds = np.concatenate(([self.min_val], inner, [self.max_val]))
         assert len(self.thresholds) == self.bins + 2
+
+    def _levels(self):
+        """Thresholds, kind and edge flag of transform (for encode_binarized)."""
+        if self.type == "thermometer":
+            return (self.thresholds if self.edge_bins else self.thresholds[1:-1]), _THERMOMETER, False
+        if self.type == "onehot":
+            return self.thresholds, _ONEHOT, self.edge_bins
+        raise ValueError(f"Unknown type: {self.type}")
 
     def _transform_thermometer(self, X):
         t = self.thresholds if self.edge_bins else self.thresholds[1:-1]

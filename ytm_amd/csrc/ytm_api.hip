@@ -188,6 +188,27 @@ void note_reload(ytm_model* m, int part) {
   }
 }
 
+// Bytes per element of a binarizer input type (YTM_DTYPE_*), 0 for none.
+size_t dtype_size(int dtype) {
+  switch (dtype) {
+    case YTM_DTYPE_U8:
+    case YTM_DTYPE_I8:
+      return 1;
+    case YTM_DTYPE_U16:
+    case YTM_DTYPE_I16:
+      return 2;
+    case YTM_DTYPE_U32:
+    case YTM_DTYPE_I32:
+    case YTM_DTYPE_F32:
+      return 4;
+    case YTM_DTYPE_I64:
+    case YTM_DTYPE_F64:
+      return 8;
+    default:
+      return 0;
+  }
+}
+
 int upload(void** dst, const void* src, size_t bytes, hipStream_t s) {
   HIP_TRY(hipMalloc(dst, bytes > 0 ? bytes : 4));
   if (bytes) HIP_TRY(hipMemcpyAsync(*dst, src, bytes, hipMemcpyHostToDevice, s));
@@ -595,6 +616,56 @@ int ytm_encode(ytm_model* m, const uint32_t* X, int64_t N, uint32_t* out) {
   m->stats.last_encode_kernel_ms = ms_total;
   (void)hipFree(dX);
   (void)hipFree(dO);
+  return rc;
+}
+
+int ytm_encode_binarized(ytm_model* m, const void* X, int x_dtype, int64_t N, const void* thresholds,
+                         int int_thresholds, int nthr, int kind, int edge_bins, uint32_t* out) {
+  if (!m || N < 0 || (N > 0 && (!X || !out)) || !thresholds) return fail(YTM_EINVAL, "bad encode arguments");
+  const size_t es = dtype_size(x_dtype);
+  if (es == 0) return fail(YTM_EINVAL, "unsupported binarizer input type");
+  if (kind != 0 && kind != 1) return fail(YTM_EINVAL, "binarizer kind must be 0 (thermometer) or 1 (one-hot)");
+  if (nthr < (kind == 1 ? 2 : 1)) return fail(YTM_EINVAL, "bad binarizer arguments");
+  if (int_thresholds && (x_dtype == YTM_DTYPE_F32 || x_dtype == YTM_DTYPE_F64))
+    return fail(YTM_EINVAL, "integer thresholds need integer input");
+  const Geom& g = m->g;
+  const int64_t width = kind == 0 ? nthr : nthr - 1 + (edge_bins ? 2 : 0);
+  if (width < 1 || g.F % width != 0)
+    return fail(YTM_EINVAL, "the binned values per sample (raw values x " + std::to_string(width) +
+                                " levels) must be dim0 * dim1 * dim2 = " + std::to_string(g.F));
+  if (N == 0) return YTM_OK;
+  const int64_t Fr = g.F / width;  // raw values per sample
+  // Chunk so that one chunk's encoded output stays below 1 GiB.
+  const int64_t chunk = std::min(std::max<int64_t>(1, ((int64_t)1 << 30) / (g.P * g.W * 4)), N);
+  void* dT = nullptr;
+  void* dX = nullptr;
+  uint32_t* dO = nullptr;
+  int rc = upload(&dT, thresholds, (size_t)nthr * 8, m->stream);
+  hipError_t e = hipSuccess;
+  if (!rc) e = hipMalloc(&dX, (size_t)(chunk * Fr) * es);
+  if (!rc && e == hipSuccess) e = hipMalloc((void**)&dO, (size_t)(chunk * g.P * g.W) * 4);
+  double ms_total = 0.0;
+  for (int64_t s = 0; !rc && e == hipSuccess && s < N; s += chunk) {
+    const int64_t n = std::min(chunk, N - s);
+    e = hipMemcpyAsync(dX, (const char*)X + (size_t)(s * Fr) * es, (size_t)(n * Fr) * es, hipMemcpyHostToDevice,
+                       m->stream);
+    if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
+    if (e == hipSuccess)
+      e = ytm::launch_encode_binned(dX, x_dtype, n, Fr, dT, int_thresholds != 0, nthr, kind == 1, edge_bins != 0, dO,
+                                    g, m->stream);
+    if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(out + s * g.P * g.W, dO, (size_t)(n * g.P * g.W) * 4, hipMemcpyDeviceToHost, m->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, m->ev0, m->ev1);
+    ms_total += ms;
+  }
+  if (!rc && e != hipSuccess) rc = fail(YTM_EHIP, std::string("encode failed: ") + hipGetErrorString(e));
+  m->stats.last_encode_kernel_ms = ms_total;
+  if (dT) (void)hipFree(dT);
+  if (dX) (void)hipFree(dX);
+  if (dO) (void)hipFree(dO);
   return rc;
 }
 
@@ -1143,25 +1214,6 @@ int ytm_get_bias(ytm_model* m, float* out) {
 // ---------------------------------------------------------------- binarizers
 namespace {
 
-size_t dtype_size(int dtype) {
-  switch (dtype) {
-    case YTM_DTYPE_U8:
-    case YTM_DTYPE_I8:
-      return 1;
-    case YTM_DTYPE_U16:
-    case YTM_DTYPE_I16:
-      return 2;
-    case YTM_DTYPE_U32:
-    case YTM_DTYPE_I32:
-    case YTM_DTYPE_F32:
-      return 4;
-    case YTM_DTYPE_I64:
-    case YTM_DTYPE_F64:
-      return 8;
-    default:
-      return 0;
-  }
-}
 
 }  // namespace
 

@@ -8,9 +8,13 @@
 // input value) are coalesced and each input value is read from the cache width times.
 // Comparisons use the type numpy promotes the operands to: double, or int64 when both the
 // data and the thresholds are integers.
+//
+// The encode fused with the binning (encode_binned_kernel) takes the raw values instead of
+// the binned uint32 array and bins each value where encode reads it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ytm_encode.h"
 #include "ytm_internal.h"
 
 namespace ytm {
@@ -24,10 +28,20 @@ __device__ __forceinline__ C as_cmp(T v) {
   return (C)v;
 }
 
-// Thermometer (binarizer.py:63-73 and the ThermometerBinarizer of :5-22): output j of
-// element i is X[i] >= t[j], j < nthr.
-// One-hot (binarizer.py:75-86): output j of element i is t[j] <= X[i] < t[j + 1], j < nthr-1;
-// with edge bins the outputs are [X[i] < t[0], those nthr - 1, X[i] >= t[nthr - 1]].
+// Level j of value v (width levels, nthr thresholds t).
+// Thermometer (binarizer.py:63-73 and the ThermometerBinarizer of :5-22): v >= t[j], j < nthr.
+// One-hot (binarizer.py:75-86): t[j] <= v < t[j + 1], j < nthr - 1; with edge bins the levels
+// are [v < t[0], those nthr - 1, v >= t[nthr - 1]].
+template <typename C, bool ONEHOT>
+__device__ __forceinline__ bool bin_level(C v, const C* __restrict__ t, int nthr, int edge, int width, int j) {
+  if (!ONEHOT) return v >= t[j];
+  if (edge && j == 0) return v < t[0];
+  if (edge && j == width - 1) return v >= t[nthr - 1];
+  const int b = edge ? j - 1 : j;
+  return v >= t[b] && v < t[b + 1];
+}
+
+// Output o of the binning: level o % width of element o / width.
 template <typename T, typename C, bool ONEHOT>
 __global__ __launch_bounds__(kBinBlock) void binarize_kernel(const T* __restrict__ X, int64_t n,
                                                              const C* __restrict__ t, int nthr, int edge,
@@ -38,20 +52,34 @@ __global__ __launch_bounds__(kBinBlock) void binarize_kernel(const T* __restrict
        o += (int64_t)gridDim.x * blockDim.x) {
     const int64_t i = o / width;
     const int j = (int)(o - i * width);
-    const C v = as_cmp<T, C>(X[i]);
-    bool r;
-    if (!ONEHOT) {
-      r = v >= t[j];
-    } else if (edge && j == 0) {
-      r = v < t[0];
-    } else if (edge && j == width - 1) {
-      r = v >= t[nthr - 1];
-    } else {
-      const int b = edge ? j - 1 : j;
-      r = v >= t[b] && v < t[b + 1];
-    }
-    out[o] = r ? 1u : 0u;
+    out[o] = bin_level<C, ONEHOT>(as_cmp<T, C>(X[i]), t, nthr, edge, width, j) ? 1u : 0u;
   }
+}
+
+// Pixel values of the fused encode: binned value f of a sample is level f % width of its raw
+// value f / width, the layout of the binarizers' outputs (the levels of a value last, so that
+// binarize_rgb's channel-major c * ch + j is level j of channel c).
+template <typename T, typename C, bool ONEHOT>
+struct BinnedPixels {
+  const T* X;
+  int64_t Fr;  // raw values per sample
+  const C* t;
+  int nthr, edge, width;
+  __device__ __forceinline__ bool operator()(int64_t e, int64_t f) const {
+    const int64_t i = f / width;
+    const int j = (int)(f - i * width);
+    return bin_level<C, ONEHOT>(as_cmp<T, C>(X[e * Fr + i]), t, nthr, edge, width, j);
+  }
+};
+
+// encode of the binned raw values of N samples (encode_words, ytm_encode.h): the same words
+// as binning them (binarize_kernel) and encoding the result.
+template <typename T, typename C, bool ONEHOT>
+__global__ __launch_bounds__(256) void encode_binned_kernel(const T* __restrict__ X, int64_t N, int64_t Fr,
+                                                            const C* __restrict__ t, int nthr, int edge,
+                                                            uint32_t* __restrict__ out, Geom g) {
+  const int width = ONEHOT ? nthr - 1 + (edge ? 2 : 0) : nthr;
+  encode_words(BinnedPixels<T, C, ONEHOT>{X, Fr, t, nthr, edge, width}, N, out, g);
 }
 
 // Collapse of binned rows (binarizer.py:88-105): thermometer -> index of the last non-zero
@@ -112,7 +140,41 @@ hipError_t launch_typed(const void* X, int dtype, int64_t n, const C* t, int nth
   return hipGetLastError();
 }
 
+template <typename C, bool ONEHOT>
+hipError_t launch_encode_typed(const void* X, int dtype, int64_t N, int64_t Fr, const C* t, int nthr, int edge,
+                               uint32_t* out, const Geom& g, hipStream_t s) {
+  const int grid = grid_of(N * g.P * g.W);
+#define YTM_ENC_CASE(code, T)                                                                          \
+  case code:                                                                                           \
+    encode_binned_kernel<T, C, ONEHOT><<<grid, 256, 0, s>>>((const T*)X, N, Fr, t, nthr, edge, out, g); \
+    break;
+  switch (dtype) {
+    YTM_ENC_CASE(YTM_DTYPE_U8, uint8_t)
+    YTM_ENC_CASE(YTM_DTYPE_I8, int8_t)
+    YTM_ENC_CASE(YTM_DTYPE_U16, uint16_t)
+    YTM_ENC_CASE(YTM_DTYPE_I16, int16_t)
+    YTM_ENC_CASE(YTM_DTYPE_U32, uint32_t)
+    YTM_ENC_CASE(YTM_DTYPE_I32, int32_t)
+    YTM_ENC_CASE(YTM_DTYPE_I64, int64_t)
+    YTM_ENC_CASE(YTM_DTYPE_F32, float)
+    YTM_ENC_CASE(YTM_DTYPE_F64, double)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef YTM_ENC_CASE
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_encode_binned(const void* X, int dtype, int64_t N, int64_t Fr, const void* t, bool int_thresholds,
+                                int nthr, bool onehot, int edge, uint32_t* out, const Geom& g, hipStream_t s) {
+  if (int_thresholds)
+    return onehot ? launch_encode_typed<int64_t, true>(X, dtype, N, Fr, (const int64_t*)t, nthr, edge, out, g, s)
+                  : launch_encode_typed<int64_t, false>(X, dtype, N, Fr, (const int64_t*)t, nthr, edge, out, g, s);
+  return onehot ? launch_encode_typed<double, true>(X, dtype, N, Fr, (const double*)t, nthr, edge, out, g, s)
+                : launch_encode_typed<double, false>(X, dtype, N, Fr, (const double*)t, nthr, edge, out, g, s);
+}
 
 hipError_t launch_binarize(const void* X, int dtype, int64_t n, const void* t, bool int_thresholds, int nthr,
                            bool onehot, int edge, uint32_t* out, hipStream_t s) {

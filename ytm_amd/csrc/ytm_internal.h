@@ -64,6 +64,11 @@ hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64
 // collapse of binned rows; see ytm_binarize / ytm_collapse_bins in ytm.h.
 hipError_t launch_binarize(const void* X, int dtype, int64_t n, const void* t, bool int_thresholds, int nthr,
                            bool onehot, int edge, uint32_t* out, hipStream_t s);
+// encode (launch_encode) of N samples of Fr raw values each (dtype YTM_DTYPE_*), each value
+// binned into the levels of launch_binarize (width = nthr, or nthr - 1 + 2 edge for one-hot;
+// g.F = Fr * width) where encode reads it; t: thresholds in device memory.
+hipError_t launch_encode_binned(const void* X, int dtype, int64_t N, int64_t Fr, const void* t, bool int_thresholds,
+                                int nthr, bool onehot, int edge, uint32_t* out, const Geom& g, hipStream_t s);
 hipError_t launch_collapse_bins(const uint32_t* B, int64_t rows, int64_t width, bool onehot, int edge, int64_t* out,
                                 hipStream_t s);
 

@@ -10,62 +10,17 @@
 #include <type_traits>
 
 #include "ytm_device.h"
+#include "ytm_encode.h"
 #include "ytm_internal.h"
 #include "ytm_train.h"
 
 namespace ytm {
 
 // ============================================================================ encode
-// One thread per output word (e, p, w); every bit is the closed form of what
-// encode_batch (src/cutm/cuda/kernel.cu:76-152) leaves in that bit:
-//   negated literal l+L/2 = NOT positive literal l (the prefilled negated half is cleared
-//   exactly where a positive bit is set); positives are the y/x thermometers and the
-//   patch pixels; bits >= L stay 0 (the reference memsets the output first).
-__device__ __forceinline__ uint32_t positive_literal(const uint32_t* Xe, const Geom& g, int64_t li,
-                                                     int64_t py, int64_t px) {
-  const int64_t ty = g.dim1 - g.pd1, tx = g.dim0 - g.pd0;
-  int64_t idx = li;
-  bool therm = false;
-  if (g.encode_loc) {
-    if (li < ty) return li < py ? 1u : 0u;
-    if (li < ty + tx) return (li - ty) < px ? 1u : 0u;
-    idx = li - ty - tx;
-  } else {
-    // The thermometer loops of kernel.cu:101-121 run even without ENCODE_LOC and write
-    // over the first pixel literals; reproduced as-is.
-    therm = (li < py) || (li >= ty && li < ty + px);
-  }
-  const int64_t row = (int64_t)g.pd0 * g.dim2;
-  const int64_t ry = idx / row, rem = idx % row;
-  const int64_t rx = rem / g.dim2, z = rem % g.dim2;
-  const uint32_t v = Xe[(py + ry) * ((int64_t)g.dim0 * g.dim2) + (px + rx) * g.dim2 + z];
-  return (v > 0u || therm) ? 1u : 0u;
-}
-
+// One thread per output word (encode_words, ytm_encode.h).
 __global__ __launch_bounds__(256) void encode_kernel(const uint32_t* __restrict__ X, int64_t N,
                                                      uint32_t* __restrict__ out, Geom g) {
-  const int64_t total = N * g.P * g.W;
-  const int64_t xw = g.dim0 - g.pd0 + 1;
-  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t w = idx % g.W;
-    const int64_t ep = idx / g.W;
-    const int64_t p = ep % g.P, e = ep / g.P;
-    const int64_t py = p / xw, px = p % xw;
-    const uint32_t* Xe = X + e * g.F;
-    uint32_t word = 0u;
-    for (int b = 0; b < 32; ++b) {
-      const int64_t l = w * 32 + b;
-      if (l >= g.L) break;
-      uint32_t bit;
-      if (g.append_negated && l >= g.Lh)
-        bit = positive_literal(Xe, g, l - g.Lh, py, px) ^ 1u;
-      else
-        bit = positive_literal(Xe, g, l, py, px);
-      word |= bit << b;
-    }
-    out[idx] = word;
-  }
+  encode_words(PlainPixels{X, g.F}, N, out, g);
 }
 
 // Literal-major copy of encoded samples with several patches: bit b of XT[e][l][j] is
