@@ -196,8 +196,9 @@ int ytm_score_dataset(ytm_model *m, const ytm_dataset *ds, float *class_sums);
  * serving loops, harnesses that forbid hipMalloc).  d_class_sums is a DEVICE pointer to
  * float (N, classes), written with the same values ytm_score_dataset returns.  The
  * kernels' literal lists and int64 class-sum accumulators live in a static per-GPU scratch
- * array of YTM_NOALLOC_SCRATCH_BYTES (32 MiB; each GPU that runs this holds it until the
- * process ends); samples go through in passes that fit it.  YTM_EINVAL when the model's
+ * array of YTM_NOALLOC_SCRATCH_BYTES (32 MiB; it is part of libytm's code object, so every
+ * GPU on which the library's kernels are loaded holds it until the process ends, whether or
+ * not this entry point is called there); samples go through in passes that fit it.  YTM_EINVAL when the model's
  * lists plus one sample's accumulators do not fit (e.g. one-patch models of more than
  * about 65000 wide clauses).  Calls on one GPU share the array, so overlapping calls
  * would race: the library serialises them per GPU with a lock.  Synchronous on return. */

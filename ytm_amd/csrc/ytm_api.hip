@@ -60,6 +60,7 @@ struct ytm_dataset {
   int64_t N;
   uint32_t* d_XT;  // [N][L][ceil(P/32)] literal-major copy (several patches), or null
   int xt_halves;   // d_XT's literals Lh..L-1 are the complements of 0..Lh-1 (TrainArgs::xt_halves)
+  uint32_t* d_order;  // [kOrderBuckets][W] literal order of the training lists (with d_XT), or null
 };
 
 namespace {
@@ -673,7 +674,7 @@ int ytm_dataset_create(ytm_model* m, const uint32_t* encX, const int32_t* encY, 
   if (!m || !out || N < 0 || (N > 0 && !encX)) return fail(YTM_EINVAL, "bad dataset arguments");
   *out = nullptr;
   const Geom& g = m->g;
-  ytm_dataset* ds = new ytm_dataset{m, nullptr, nullptr, N, nullptr, 0};
+  ytm_dataset* ds = new ytm_dataset{m, nullptr, nullptr, N, nullptr, 0, nullptr};
   int rc = upload((void**)&ds->d_X, encX, (size_t)(N * g.P * g.W) * 4, m->stream);
   if (!rc && encY) rc = upload((void**)&ds->d_Y, encY, (size_t)(N * g.K) * 4, m->stream);
   if (!rc && ytm::literal_major(g) && N > 0) {
@@ -681,6 +682,9 @@ int ytm_dataset_create(ytm_model* m, const uint32_t* encX, const int32_t* encY, 
     const size_t bytes = (size_t)(N * g.L * ((g.P + 31) / 32)) * 4;
     hipError_t e = hipMalloc(&ds->d_XT, bytes);
     if (e == hipSuccess) e = ytm::launch_transpose(ds->d_X, N, ds->d_XT, g, m->stream);
+    // the order of the training kernels' literal lists, from the densities of the first samples
+    if (e == hipSuccess) e = hipMalloc(&ds->d_order, (size_t)ytm::kOrderBuckets * g.W * 4);
+    if (e == hipSuccess) e = ytm::launch_literal_order(nullptr, ds->d_XT, N, g, ds->d_order, m->stream);
     if (e == hipSuccess && g.append_negated) {
       // Encoded samples hold the negations as complements (BaseTM.encode); samples encoded
       // elsewhere may not, so the training kernels rely on it only where this check holds.
@@ -713,6 +717,7 @@ void ytm_dataset_destroy(ytm_dataset* ds) {
   if (ds->d_X) (void)hipFree(ds->d_X);
   if (ds->d_Y) (void)hipFree(ds->d_Y);
   if (ds->d_XT) (void)hipFree(ds->d_XT);
+  if (ds->d_order) (void)hipFree(ds->d_order);
   delete ds;
 }
 
@@ -850,6 +855,8 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     a.stream_gens = sg_env ? std::max(0, std::atoi(sg_env)) : 0;
     const char* xh_env = std::getenv("YTM_TRAIN_XT_HALVES");  // 0: stage the whole literal-major copy
     a.xt_halves = ds->xt_halves && !(xh_env && std::atoi(xh_env) == 0);
+    const char* lo_env = std::getenv("YTM_LIST_ORDER");  // 0: literal lists in index order
+    a.lit_order = (lo_env && std::atoi(lo_env) == 0) ? nullptr : ds->d_order;
     const char* tt_env = std::getenv("YTM_TRAIN_TEST_TIMEOUT");  // test hook of the timeout path
     a.test_timeout = tt_env && std::atoi(tt_env) > 0;
     a.g = g;

@@ -33,6 +33,10 @@ hipError_t launch_score_tile(const uint32_t* planes, const int32_t* ninc, const 
                              int64_t N, const Geom& g, long long* parts, double w_bound, hipStream_t s);
 hipError_t launch_score_parts_finish(const long long* parts, int64_t nch, const float* bias, int64_t N, const Geom& g,
                                      float* out, hipStream_t s);
+// Literal order of the literal lists, order [kOrderBuckets][W], from the densities of the
+// first min(N, kOrderSamples) samples of XT (literal-major) when given, else of X.
+hipError_t launch_literal_order(const uint32_t* X, const uint32_t* XT, int64_t N, const Geom& g, uint32_t* order,
+                                hipStream_t s);
 // Scoring of several-patch models on literal-major samples; scratch holds score_lists_bytes(g)
 // (0: not available for this geometry).
 size_t score_lists_bytes(const Geom& g);

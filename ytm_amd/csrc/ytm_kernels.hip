@@ -291,15 +291,62 @@ __global__ __launch_bounds__(256) void score_tile_kernel(const uint32_t* __restr
   }
 }
 
-// Several patches: the included literals of every clause as a list (build_literal_list),
-// [C][cap] with the include counts [C]; one wave per clause.
+// Literal order of the list walks (build_literal_list): the density of literal l over the
+// first S samples, the share of their (sample, patch) pairs where l is 1, from the
+// literal-major copy XT ([N][L][PW]) when given, else from X ([N][P][W]); literal l goes to
+// bucket min(kOrderBuckets - 1, density * kOrderBuckets), literals past L to the last.  A
+// block of 4 waves takes 64 literals (two words of the order), each wave a quarter of the
+// rows.
+__global__ __launch_bounds__(256) void literal_order_kernel(const uint32_t* __restrict__ X,
+                                                            const uint32_t* __restrict__ XT, int64_t S, Geom g,
+                                                            uint32_t* __restrict__ order) {
+  __shared__ int64_t s_cnt[4][kWave];
+  const int lane = lane_id(), part = threadIdx.x / kWave;
+  const int64_t l = (int64_t)blockIdx.x * kWave + lane;
+  const int64_t PW = (g.P + 31) / 32;
+  int64_t cnt = 0;
+  if (l < g.L) {
+    if (XT) {
+      for (int64_t e = part; e < S; e += 4)
+        for (int64_t j = 0; j < PW; ++j) cnt += __popc(XT[(e * g.L + l) * PW + j]);
+    } else {
+      for (int64_t r = part; r < S * g.P; r += 4) cnt += (X[r * g.W + l / 32] >> (l % 32)) & 1u;
+    }
+  }
+  s_cnt[part][lane] = cnt;
+  __syncthreads();
+  if (part != 0) return;
+  const int64_t total = s_cnt[0][lane] + s_cnt[1][lane] + s_cnt[2][lane] + s_cnt[3][lane];
+  const int64_t pairs = S * g.P;
+  int b = pairs > 0 ? (int)(total * kOrderBuckets / pairs) : 0;
+  b = (l >= g.L || b >= kOrderBuckets) ? kOrderBuckets - 1 : b;
+  for (int k = 0; k < kOrderBuckets; ++k) {
+    const unsigned long long bal = __ballot(b == k);
+    const int64_t w0 = 2 * (int64_t)blockIdx.x;
+    if (lane == 0 && w0 < g.W) order[k * g.W + w0] = (uint32_t)bal;
+    if (lane == 0 && w0 + 1 < g.W) order[k * g.W + w0 + 1] = (uint32_t)(bal >> 32);
+  }
+}
+
+// The buckets of literal_order_kernel from the first min(N, kOrderSamples) samples.
+hipError_t launch_literal_order(const uint32_t* X, const uint32_t* XT, int64_t N, const Geom& g, uint32_t* order,
+                                hipStream_t s) {
+  const int64_t S = N < kOrderSamples ? N : kOrderSamples;
+  literal_order_kernel<<<(unsigned)((g.W + 1) / 2), 256, 0, s>>>(X, XT, S, g, order);
+  return hipGetLastError();
+}
+
+// The included literals of every clause as a list (build_literal_list) in the order of
+// `order` (null: literal index order), [C][cap] with the include counts [C]; one wave per
+// clause.
 __global__ __launch_bounds__(256) void build_lists_kernel(const uint32_t* __restrict__ planes, Geom g, int cap,
+                                                          const uint32_t* __restrict__ order,
                                                           uint16_t* __restrict__ lists, int32_t* __restrict__ nlit) {
   const int lane = lane_id();
   const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / kWave;
   const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
   for (int64_t c = wave; c < g.C; c += nwaves) {
-    const int n = build_literal_list(g, planes + (c * g.np + g.np - 1) * g.W, lists + c * cap, cap);
+    const int n = build_literal_list(g, planes + (c * g.np + g.np - 1) * g.W, lists + c * cap, cap, order);
     if (lane == 0) nlit[c] = n;
   }
 }
@@ -308,9 +355,9 @@ __global__ __launch_bounds__(256) void build_lists_kernel(const uint32_t* __rest
 // lv (the list padded to a multiple of 8).  With at least two groups of PW lanes in the wave
 // (the bitmap's PW words), group gq takes the runs 8(it * NG + gq) of step it, fetching
 // them from their lanes with ds_bpermute, and the groups' bitmaps are AND-ed at the end
-// (as firing_from_list); otherwise the runs are read 8 at a time with readlane.  SCALED:
-// the entries are byte offsets (lists_scaled).
-template <bool SCALED>
+// (as firing_from_list); otherwise the runs are read 8 at a time with readlane.  FORM:
+// list_form(g).
+template <int FORM>
 __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 lv, int n, const uint32_t* xt,
                                                           uint32_t acc) {
   const int lane = lane_id();
@@ -330,10 +377,18 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
                              (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.y),
                              (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.z),
                              (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)lv.w)};
-      if (in_group && run < nruns) part &= and_listed_as<SCALED>(g, e, xt, (uint32_t)w);
-      const unsigned long long live = __ballot(part != 0u);
-      bool dead = false;
-      for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * GS)) & gmask) == 0ull;
+      if (in_group && run < nruns) part &= and_listed_as<FORM>(g, e, xt, (uint32_t)w);
+      // the walk ends when nothing fires: with two groups (the 32-lane halves) when the AND
+      // of both partials is empty (the halves' words meet through one lane swap), else
+      // when some group's partial is empty
+      bool dead;
+      if (NG == 2) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(part, part, false, false);
+        dead = !__any((sw[0] & sw[1]) != 0u);
+      } else {
+        const unsigned long long live = __ballot(part != 0u);
+        dead = __any(in_group && ((live >> (q * GS)) & gmask) == 0ull);
+      }
       if (dead) {
         part = 0u;
         break;
@@ -349,7 +404,7 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
     const int src = j >> 3;
     const uint32_t qv[4] = {(uint32_t)lane_value((int)lv.x, src), (uint32_t)lane_value((int)lv.y, src),
                             (uint32_t)lane_value((int)lv.z, src), (uint32_t)lane_value((int)lv.w, src)};
-    acc &= and_listed_as<SCALED>(g, qv, xt, (uint32_t)jl);
+    acc &= and_listed_as<FORM>(g, qv, xt, (uint32_t)jl);
     if ((j & 8) && !__any(acc != 0u)) break;
   }
   return acc;
@@ -369,6 +424,7 @@ constexpr int kScoreListCap = 256;
 constexpr int kScoreLmThreads = 1024;
 inline int score_lm_threads(const Geom& g) { return (g.L * ((g.P + 31) / 32)) * 4 > 32 * 1024 ? 1024 : 256; }
 
+template <int FORM>
 __global__ __launch_bounds__(kScoreLmThreads) void score_lm_kernel(const uint32_t* __restrict__ planes,
                                                        const uint16_t* __restrict__ lists,
                                                        const int32_t* __restrict__ nlit, const float* __restrict__ w,
@@ -376,10 +432,10 @@ __global__ __launch_bounds__(kScoreLmThreads) void score_lm_kernel(const uint32_
                                                        long long* __restrict__ acc) {
   extern __shared__ uint32_t s_xts[];  // [L][PW]
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave, nwv = blockDim.x / kWave;
+  // wave-uniform in a scalar register, so that the clause loop and its loads are scalar
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)), nwv = blockDim.x / kWave;
   const int64_t xtw = g.L * ((g.P + 31) / 32);
   const int64_t nch = (g.C + kScoreLmChunk - 1) / kScoreLmChunk;
-  const bool scaled = lists_scaled(g);
   for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
     const int64_t e = blk / nch, ch = blk % nch;
     const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
@@ -393,8 +449,7 @@ __global__ __launch_bounds__(kScoreLmThreads) void score_lm_kernel(const uint32_
       uint32_t fire = all_patches_word(g);
       if (n <= kScoreListCap) {
         const uint4 lv = 8 * lane < n ? *(const uint4*)(lists + c * kScoreListCap + 8 * lane) : uint4{0u, 0u, 0u, 0u};
-        fire = scaled ? firing_from_list_regs<true>(g, lv, n, s_xts, fire)
-                      : firing_from_list_regs<false>(g, lv, n, s_xts, fire);
+        fire = firing_from_list_regs<FORM>(g, lv, n, s_xts, fire);
       } else {
         fire = firing_from_mask(g, planes + (c * g.np + g.np - 1) * g.W, s_xts, fire);
       }
@@ -557,7 +612,7 @@ __global__ __launch_bounds__(256) void tile_kernel(const uint32_t* __restrict__ 
 // firing bitmap over all patches is the AND of the included literals' bitsets (from the
 // clause's literal list when it has one).  MODE 0: out[e][c] = some patch fires;
 // MODE 1: out[e][c][p]; MODE 2: out[e][c][j] with bit b = patch 32j + b (0 beyond P).
-template <int MODE>
+template <int MODE, int FORM>
 __global__ __launch_bounds__(kScoreLmThreads) void transform_lm_kernel(const uint32_t* __restrict__ planes,
                                                            const uint16_t* __restrict__ lists,
                                                            const int32_t* __restrict__ nlit,
@@ -565,11 +620,10 @@ __global__ __launch_bounds__(kScoreLmThreads) void transform_lm_kernel(const uin
                                                            uint32_t* __restrict__ out) {
   extern __shared__ uint32_t s_xts[];  // [L][PW]
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave, nwv = blockDim.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)), nwv = blockDim.x / kWave;
   const int PW = (int)((g.P + 31) / 32);
   const int64_t xtw = g.L * PW;
   const int64_t nch = (g.C + kScoreLmChunk - 1) / kScoreLmChunk;
-  const bool scaled = lists_scaled(g);
   for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
     const int64_t e = blk / nch, ch = blk % nch;
     const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
@@ -583,8 +637,7 @@ __global__ __launch_bounds__(kScoreLmThreads) void transform_lm_kernel(const uin
         if (n <= kScoreListCap) {
           const uint4 lv =
               8 * lane < n ? *(const uint4*)(lists + c * kScoreListCap + 8 * lane) : uint4{0u, 0u, 0u, 0u};
-          fire = scaled ? firing_from_list_regs<true>(g, lv, n, s_xts, fire)
-                        : firing_from_list_regs<false>(g, lv, n, s_xts, fire);
+          fire = firing_from_list_regs<FORM>(g, lv, n, s_xts, fire);
         } else {
           fire = firing_from_mask(g, planes + (c * g.np + g.np - 1) * g.W, s_xts, fire);
         }
@@ -913,24 +966,56 @@ static bool tile_fits(const Geom& g, int mode) {
   return g.P == 1 && g.W <= 64 && (mode == 1 || g.K <= kTileMaxK);
 }
 
-size_t score_lists_bytes(const Geom& g) {
-  if (!literal_major(g) || g.L > 65535 || (size_t)(g.L * ((g.P + 31) / 32)) * 4 > 120 * 1024) return 0;
-  return (size_t)g.C * kScoreListCap * 2 + (size_t)g.C * 4;
+// Scratch of the list-based scorers: lists [C][kScoreListCap] uint16, include counts [C]
+// int32, literal order [kOrderBuckets][W] uint32.
+static size_t lists_scratch_bytes(const Geom& g) {
+  return (size_t)g.C * kScoreListCap * 2 + (size_t)g.C * 4 + (size_t)kOrderBuckets * g.W * 4;
+}
+struct ListScratch {
+  uint16_t* lists;
+  int32_t* nlit;
+  uint32_t* order;
+};
+static ListScratch list_scratch(void* scratch, const Geom& g) {
+  ListScratch r;
+  r.lists = (uint16_t*)scratch;
+  r.nlit = (int32_t*)(r.lists + g.C * kScoreListCap);
+  r.order = (uint32_t*)(r.nlit + g.C);
+  return r;
 }
 
-size_t score_wide_bytes(const Geom& g) {
-  return score_wide_fits(g) ? (size_t)g.C * kScoreListCap * 2 + (size_t)g.C * 4 : 0;
+size_t score_lists_bytes(const Geom& g) {
+  if (!literal_major(g) || g.L > 65535 || (size_t)(g.L * ((g.P + 31) / 32)) * 4 > 120 * 1024) return 0;
+  return lists_scratch_bytes(g);
+}
+
+size_t score_wide_bytes(const Geom& g) { return score_wide_fits(g) ? lists_scratch_bytes(g) : 0; }
+
+// Literal order from the batch, then the lists in that order.
+static hipError_t build_lists(const uint32_t* planes, const uint32_t* X, const uint32_t* XT, int64_t N,
+                              const Geom& g, const ListScratch& ls, hipStream_t s) {
+  hipError_t e = launch_literal_order(X, XT, N, g, ls.order, s);
+  if (e != hipSuccess) return e;
+  build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, ls.order, ls.lists,
+                                                                  ls.nlit);
+  return hipGetLastError();
 }
 
 hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_t* XT, int64_t N, const Geom& g,
                            void* scratch, long long* acc, hipStream_t s) {
-  uint16_t* lists = (uint16_t*)scratch;
-  int32_t* nlit = (int32_t*)(lists + g.C * kScoreListCap);
-  build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
+  const ListScratch ls = list_scratch(scratch, g);
+  hipError_t err = build_lists(planes, nullptr, XT, N, g, ls, s);
+  if (err != hipSuccess) return err;
+  uint16_t* lists = ls.lists;
+  int32_t* nlit = ls.nlit;
   const int64_t blocks = N * ((g.C + kScoreLmChunk - 1) / kScoreLmChunk);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
-  score_lm_kernel<<<grid, score_lm_threads(g), (size_t)(g.L * ((g.P + 31) / 32)) * 4, s>>>(planes, lists, nlit, w, XT,
-                                                                                         N, g, acc);
+  const size_t lds = (size_t)(g.L * ((g.P + 31) / 32)) * 4;
+  // the sample fits LDS (score_lists_bytes), so its word offsets fit 16 bits: no kListIndex
+  if (list_form(g) == kListBytes)
+    score_lm_kernel<kListBytes><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, w, XT, N, g, acc);
+  else
+    score_lm_kernel<kListWords><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, w, XT, N, g, acc);
   return hipGetLastError();
 }
 
@@ -942,9 +1027,11 @@ bool score_wide_fits(const Geom& g) {
 
 hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint32_t* X, int64_t N, const Geom& g,
                              void* scratch, long long* acc, hipStream_t s) {
-  uint16_t* lists = (uint16_t*)scratch;
-  int32_t* nlit = (int32_t*)(lists + g.C * kScoreListCap);
-  build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
+  const ListScratch ls = list_scratch(scratch, g);
+  hipError_t err = build_lists(planes, X, nullptr, N, g, ls, s);
+  if (err != hipSuccess) return err;
+  uint16_t* lists = ls.lists;
+  int32_t* nlit = ls.nlit;
   // enough blocks to fill the device (two per CU fit): split the clauses when tiles are few
   const int64_t tiles = (N + kWideTile - 1) / kWideTile;
   const int64_t want = (512 + tiles - 1) / tiles, most = (g.C + 1023) / 1024;
@@ -958,10 +1045,13 @@ hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint3
 
 hipError_t launch_transform_wide(const uint32_t* planes, const uint32_t* X, int64_t N, const Geom& g, void* scratch,
                                  bool lists_ready, uint32_t* out, hipStream_t s) {
-  uint16_t* lists = (uint16_t*)scratch;
-  int32_t* nlit = (int32_t*)(lists + g.C * kScoreListCap);
-  if (!lists_ready)
-    build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
+  const ListScratch ls = list_scratch(scratch, g);
+  if (!lists_ready) {
+    hipError_t err = build_lists(planes, X, nullptr, N, g, ls, s);
+    if (err != hipSuccess) return err;
+  }
+  uint16_t* lists = ls.lists;
+  int32_t* nlit = ls.nlit;
   const int64_t tiles = (N + kWideTile - 1) / kWideTile;
   const int64_t want = (512 + tiles - 1) / tiles, most = (g.C + 1023) / 1024;
   const int64_t nch = want < most ? want : most;
@@ -1029,19 +1119,28 @@ hipError_t launch_transform(const uint32_t* planes, const int32_t* ninc, const u
 
 hipError_t launch_transform_lm(const uint32_t* planes, const uint32_t* XT, int64_t N, const Geom& g, int mode,
                                void* scratch, bool lists_ready, uint32_t* out, hipStream_t s) {
-  uint16_t* lists = (uint16_t*)scratch;
-  int32_t* nlit = (int32_t*)(lists + g.C * kScoreListCap);
-  if (!lists_ready)
-    build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, lists, nlit);
+  const ListScratch ls = list_scratch(scratch, g);
+  if (!lists_ready) {
+    hipError_t err = build_lists(planes, nullptr, XT, N, g, ls, s);
+    if (err != hipSuccess) return err;
+  }
+  uint16_t* lists = ls.lists;
+  int32_t* nlit = ls.nlit;
   const int64_t blocks = N * ((g.C + kScoreLmChunk - 1) / kScoreLmChunk);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
   const size_t lds = (size_t)(g.L * ((g.P + 31) / 32)) * 4;
-  if (mode == 0)
-    transform_lm_kernel<0><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, XT, N, g, out);
-  else if (mode == 1)
-    transform_lm_kernel<1><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, XT, N, g, out);
-  else
-    transform_lm_kernel<2><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, XT, N, g, out);
+  const int th = score_lm_threads(g);
+  const bool bytes = list_form(g) == kListBytes;  // else kListWords: the sample fits LDS
+  if (mode == 0) {
+    if (bytes) transform_lm_kernel<0, kListBytes><<<grid, th, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+    else transform_lm_kernel<0, kListWords><<<grid, th, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+  } else if (mode == 1) {
+    if (bytes) transform_lm_kernel<1, kListBytes><<<grid, th, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+    else transform_lm_kernel<1, kListWords><<<grid, th, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+  } else {
+    if (bytes) transform_lm_kernel<2, kListBytes><<<grid, th, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+    else transform_lm_kernel<2, kListWords><<<grid, th, lds, s>>>(planes, lists, nlit, XT, N, g, out);
+  }
   return hipGetLastError();
 }
 

@@ -184,27 +184,46 @@ __device__ __forceinline__ uint32_t all_patches_word(const Geom& g) {
   return (lane == PW - 1 && (g.P & 31)) ? ((1u << (g.P & 31)) - 1u) : 0xFFFFFFFFu;
 }
 
-// A literal list entry of a model with several patches is the literal's byte offset in the
-// literal-major sample, l * 4 * ceil(P/32), when every such offset fits 16 bits: a list walk
-// then adds the entry to its lane's word address (one add, which reads the entry's half of
-// the packed pair in place) instead of multiplying it.  Otherwise, and for one-patch models,
-// the entry is the literal index l.
-__device__ __forceinline__ bool lists_scaled(const Geom& g) {
-  return g.P > 1 && (int64_t)(g.L - 1) * 4 * ((g.P + 31) / 32) <= 0xFFFF;
+// Form of a literal list entry, chosen per model so that a list walk turns an entry into an
+// address without a multiply (v_mul_lo_u32 runs at a quarter of the VALU rate):
+//   kListBytes: the literal's byte offset in the literal-major sample, l * 4 * ceil(P/32),
+//     when every such offset fits 16 bits (several patches): one add per entry, which reads
+//     the entry's half of the packed pair in place;
+//   kListWords: its word offset l * ceil(P/32) when that fits 16 bits (every one-patch
+//     model, where it is l): an extract and a shift-add;
+//   kListIndex: the literal index l, multiplied by ceil(P/32) in the walk (several patches
+//     whose literal-major sample exceeds 65536 words).
+constexpr int kListIndex = 0, kListWords = 1, kListBytes = 2;
+__host__ __device__ __forceinline__ int list_form(const Geom& g) {
+  const int64_t last_word = (int64_t)(g.L - 1) * ((g.P + 31) / 32);
+  if (g.P > 1 && last_word * 4 <= 0xFFFF) return kListBytes;
+  return last_word <= 0xFFFF ? kListWords : kListIndex;
+}
+__device__ __forceinline__ uint32_t list_scale(const Geom& g) {
+  const int f = list_form(g);
+  const uint32_t PW = (uint32_t)((g.P + 31) / 32);
+  return f == kListBytes ? 4u * PW : (f == kListWords ? PW : 1u);
 }
 
 // AND of word `word` of the bitsets of the 2 * NE literals whose list entries e holds (two
-// per element) in the literal-major sample xt ([L][PW] words); SCALED: lists_scaled(g).
-template <bool SCALED, int NE>
+// per element) in the literal-major sample xt ([L][PW] words); FORM: list_form(g).
+template <int FORM, int NE>
 __device__ __forceinline__ uint32_t and_listed_as(const Geom& g, const uint32_t (&e)[NE], const uint32_t* xt,
                                                   uint32_t word) {
   uint32_t v = 0xFFFFFFFFu;
-  if (SCALED) {
+  if (FORM == kListBytes) {
     const char* xb = (const char*)(xt + word);
 #pragma unroll
     for (int u = 0; u < NE; ++u) {
       v &= *(const uint32_t*)(xb + (e[u] & 0xFFFFu));
       v &= *(const uint32_t*)(xb + (e[u] >> 16));
+    }
+  } else if (FORM == kListWords) {
+    const uint32_t* xw = xt + word;
+#pragma unroll
+    for (int u = 0; u < NE; ++u) {
+      v &= xw[e[u] & 0xFFFFu];
+      v &= xw[e[u] >> 16];
     }
   } else {
     const uint32_t PW = (uint32_t)((g.P + 31) / 32);
@@ -220,37 +239,83 @@ __device__ __forceinline__ uint32_t and_listed_as(const Geom& g, const uint32_t 
 template <int NE>
 __device__ __forceinline__ uint32_t and_listed(const Geom& g, const uint32_t (&e)[NE], const uint32_t* xt,
                                                uint32_t word) {
-  return lists_scaled(g) ? and_listed_as<true>(g, e, xt, word) : and_listed_as<false>(g, e, xt, word);
+  switch (list_form(g)) {
+    case kListBytes: return and_listed_as<kListBytes>(g, e, xt, word);
+    case kListWords: return and_listed_as<kListWords>(g, e, xt, word);
+    default: return and_listed_as<kListIndex>(g, e, xt, word);
+  }
 }
 
-// Included literals of a clause (include mask m, W words), in increasing order, written to
-// list[0, n) when n <= cap (as entries: lists_scaled), the entries from n to the next
-// multiple of 8 repeating literal n-1 (cap a multiple of 8).  Returns n, the include count.
-// Wave-uniform.
-__device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* list, int cap) {
-  // 64 words at a time, one per lane: lane w writes its word's included literals from its
-  // prefix-sum offset, lowest bit first, so the list is in increasing literal order
+// Order of the literals in the lists: kOrderBuckets buckets of literal density, the share
+// of (sample, patch) pairs of a few samples where the literal is 1 (literal_order_kernel),
+// sparsest first, increasing literal index within a bucket.  A walk ends at the first step
+// whose AND leaves no patch firing, so the literals most likely to be 0 go first; the AND,
+// and so every result, is the same in any order.  order[b][w]: bit i set when literal
+// 32w + i is in bucket b; each literal of the W words is in exactly one bucket.
+// (kOrderBuckets, kOrderSamples: ytm_types.h)
+
+// One round of build_literal_list: the literals mv of word w, lane by lane in lane order,
+// appended to list[total...) (entries past cap dropped); updates total and last (the last
+// literal appended).  Wave-uniform.
+__device__ __forceinline__ void append_literals(uint32_t mv, int w, uint32_t scale, uint16_t* list, int cap,
+                                                int* total, int* last) {
+  const int pc = __popc(mv);
+  const int incl = wave_inclusive_scan(pc);
+  const int tot = lane_value(incl, kWave - 1);
+  if (tot == 0) return;
+  const unsigned long long nz = __ballot(mv != 0u);
+  const int hi = 63 - __clzll((long long)nz);  // lane of the round's last literal
+  *last = lane_value(32 * w + 31 - __clz((int)(mv | 1u)), hi);
+  int pos = *total + incl - pc;
+  while (mv) {
+    const int bit = __ffs((int)mv) - 1;
+    if (pos < cap) list[pos] = (uint16_t)((uint32_t)(32 * w + bit) * scale);
+    ++pos;
+    mv &= mv - 1u;
+  }
+  *total += tot;
+}
+
+// Included literals of a clause (include mask m, W words), bucket by bucket of `order`
+// (literal index order when order is null), written to list[0, n) when n <= cap (as
+// entries of list_form(g)), the entries from n to the next multiple of 8 repeating the
+// last one (cap a multiple of 8).  Returns n, the include count.  Wave-uniform.
+// BY_PAIRS: a round takes 64 (bucket, word) pairs in list order, one per lane, so that a
+// model of W words needs ceil(kOrderBuckets * W / 64) rounds; else a round per bucket and
+// 64 words.  The lists are the same; the kernels differ in what the inlined code costs
+// them (the resident kernel rebuilds lists on its critical path and takes pairs, the
+// global kernel rebuilds them rarely and runs its evaluation loop faster beside the
+// per-bucket form).
+template <bool BY_PAIRS = true>
+__device__ int build_literal_list(const Geom& g, const uint32_t* m, uint16_t* list, int cap,
+                                  const uint32_t* order = nullptr) {
   const int lane = lane_id();
-  const uint32_t scale = lists_scaled(g) ? 4u * (uint32_t)((g.P + 31) / 32) : 1u;
+  const uint32_t scale = list_scale(g);
+  const int W = (int)g.W;
   int total = 0, last = 0;
-  for (int64_t wb = 0; wb < g.W; wb += kWave) {
-    const int64_t w = wb + lane;
-    uint32_t mv = w < g.W ? m[w] : 0u;
-    const int pc = __popc(mv);
-    const int incl = wave_inclusive_scan(pc);
-    const int tot = lane_value(incl, kWave - 1);
-    if (tot == 0) continue;
-    const unsigned long long nz = __ballot(mv != 0u);
-    const int hi = 63 - __clzll((long long)nz);  // lane of the chunk's last included literal
-    last = lane_value((int)(32 * w) + 31 - __clz((int)(mv | 1u)), hi);
-    int pos = total + incl - pc;
-    while (mv) {
-      const int b = __ffs((int)mv) - 1;
-      if (pos < cap) list[pos] = (uint16_t)((uint32_t)(32 * w + b) * scale);
-      ++pos;
-      mv &= mv - 1u;
+  if (BY_PAIRS || !order) {
+    // lane i takes pair (bucket b, word w) of each round (the words when there is no
+    // order); a round moves it q64 buckets and r64 words on
+    const int npairs = order ? kOrderBuckets * W : W;
+    const int q64 = kWave / W, r64 = kWave - q64 * W;
+    int b = lane / W, w = lane - b * W;
+    for (int pb = 0; pb < npairs; pb += kWave) {
+      uint32_t mv = pb + lane < npairs ? m[w] : 0u;
+      if (order) mv &= pb + lane < npairs ? order[b * W + w] : 0u;
+      append_literals(mv, w, scale, list, cap, &total, &last);
+      b += q64;
+      w += r64;
+      if (w >= W) {
+        w -= W;
+        ++b;
+      }
     }
-    total += tot;
+  } else {
+    for (int b = 0; b < kOrderBuckets; ++b)
+      for (int wb = 0; wb < W; wb += kWave) {
+        const int w = wb + lane;
+        append_literals(w < W ? m[w] & order[b * W + w] : 0u, w, scale, list, cap, &total, &last);
+      }
   }
   if (total > 0 && total <= cap) {
     const int pad_end = ((total + 7) & ~7) < cap ? ((total + 7) & ~7) : cap;
@@ -292,9 +357,17 @@ __device__ __forceinline__ uint32_t firing_from_list(const Geom& g, const uint16
         const uint32_t w8[8] = {q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
         part &= and_listed(g, w8, xt, (uint32_t)w);
       }
-      const unsigned long long live = __ballot(part != 0u);
-      bool dead = false;
-      for (int gq = 0; gq < NG; ++gq) dead = dead || ((live >> (gq * GS)) & gmask) == 0ull;
+      // the walk ends when nothing fires: with two groups (the 32-lane halves) when the AND
+      // of both partials is empty (the halves' words meet through one lane swap), else
+      // when some group's partial is empty
+      bool dead;
+      if (NG == 2) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(part, part, false, false);
+        dead = !__any((sw[0] & sw[1]) != 0u);
+      } else {
+        const unsigned long long live = __ballot(part != 0u);
+        dead = __any(in_group && ((live >> (q * GS)) & gmask) == 0ull);
+      }
       if (dead) {
         part = 0u;
         break;
@@ -1283,8 +1356,8 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         s_mask[(int64_t)idx * g.W + w] = a.planes[(c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W + w];
   if (cap > 0)  // literal lists of the own clauses (visible after the first barrier below)
     for (int idx = wave; idx < n_own; idx += nwv) {
-      const int n = build_literal_list(g, a.planes + (c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W,
-                                       s_lits + (int64_t)idx * cap, cap);
+      const int n = build_literal_list<false>(g, a.planes + (c_begin + idx) * cw + (int64_t)(g.np - 1) * g.W,
+                                       s_lits + (int64_t)idx * cap, cap, a.lit_order);
       if (lane == 0) s_nlit[idx] = n;
     }
   // The LDS copy of sample j (threads [first, first + count)): literal-major words, or with
@@ -1506,7 +1579,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         const int64_t c = c_begin + idx;
         const uint32_t* top = a.planes + c * cw + (int64_t)(g.np - 1) * g.W;
         if (cap > 0) {
-          const int n = build_literal_list(g, top, s_lits + (int64_t)idx * cap, cap);
+          const int n = build_literal_list<false>(g, top, s_lits + (int64_t)idx * cap, cap, a.lit_order);
           if (lane == 0) s_nlit[idx] = n;
         }
         if (!more) continue;
@@ -1933,7 +2006,8 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
   __syncthreads();
   if (cap > 0) {
     for (int idx = wave; idx < n_own; idx += nwv) {
-      const int n = build_literal_list(g, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W, s_lits + (int64_t)idx * cap, cap);
+      const int n = build_literal_list(g, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W, s_lits + (int64_t)idx * cap,
+                                       cap, a.lit_order);
       if (lane == 0) s_nlit[idx] = n;
     }
     __syncthreads();
@@ -2262,7 +2336,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
           for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk) {
             const int idx = s_task_idx[tk];
             const int n = build_literal_list(g, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W,
-                                             s_lits + (int64_t)idx * cap, cap);
+                                             s_lits + (int64_t)idx * cap, cap, a.lit_order);
             if (lane == 0) s_nlit[idx] = n;
           }
         if (more)
@@ -2283,7 +2357,7 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
                           have ? s_rng + (int64_t)sb * g.W * (kPreGroups * 4) : nullptr);
         if (cap > 0) {
           const int n = build_literal_list(g, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W,
-                                           s_lits + (int64_t)idx * cap, cap);
+                                           s_lits + (int64_t)idx * cap, cap, a.lit_order);
           if (lane == 0) s_nlit[idx] = n;
         }
         if (more)

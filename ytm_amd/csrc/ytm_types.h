@@ -79,6 +79,11 @@ constexpr int kStreamDepth = 32;
 constexpr int kStreamClauses = 64;
 __host__ __device__ constexpr int64_t stream_rows(int64_t n) { return n * (kStreamDepth + 1); }
 
+// Literal order of the literal lists: buckets of literal density, and the samples whose
+// densities set them (build_literal_list, literal_order_kernel).
+constexpr int kOrderBuckets = 8;
+constexpr int kOrderSamples = 32;
+
 struct TrainArgs {
   uint32_t* planes;          // [C][np][W]
   float* weights;            // [C][K]
@@ -107,6 +112,7 @@ struct TrainArgs {
   int test_timeout;          // test hook: class-sum waits never see their sums and expire at once
   int xt_halves;             // XT's literals Lh..L-1 are the complements of 0..Lh-1 (checked per dataset)
   int stream_gens;           // streaming kernel: stops per stream before fresh rows (0: as many as fit; test hook)
+  const uint32_t* lit_order; // [kOrderBuckets][W] order of the literal lists (build_literal_list), or null
   Geom g;
 };
 
