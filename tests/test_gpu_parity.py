@@ -322,16 +322,27 @@ def test_fit_variant_flags(opts):
 @pytest.mark.parametrize("case", [
     dict(dim=(16, 1, 1), n_classes=64, clauses=64, n=160),                           # 64 classes: a lane per class
     dict(dim=(20, 1, 1), n_classes=3, clauses=40, n=120, number_of_ta_states=65535),  # 16 state bit-planes
+    dict(dim=(20, 1, 1), n_classes=3, clauses=40, n=120, number_of_ta_states=(1 << 20) + 3),  # 21 bit-planes
+    dict(dim=(20, 1, 1), n_classes=3, clauses=40, n=120, number_of_ta_states=2**31 - 1),  # 31: the int32 maximum
     dict(dim=(66, 66, 1), patch_dim=(3, 3), n_classes=2, clauses=16, n=3),            # 4096 patches (no literal-major copy)
+    # beyond the persistent kernels: a launch per sample, decisions 64 classes at a time
+    dict(dim=(16, 1, 1), n_classes=65, clauses=40, n=200),
+    dict(dim=(12, 1, 1), n_classes=150, clauses=30, n=300),
+    dict(dim=(8, 8, 1), patch_dim=(3, 3), n_classes=70, clauses=20, n=40),
+    dict(dim=(16, 1, 1), n_classes=70, clauses=2, n=200, coalesced=False),
+    # more patches than 64 chunks of 64: the reservoir's patch found in a second pass
+    dict(dim=(70, 70, 1), patch_dim=(3, 3), n_classes=2, clauses=12, n=3),
+    dict(dim=(130, 130, 1), patch_dim=(2, 2), n_classes=3, clauses=4, n=2),
 ])
 def test_supported_limits(case):
-    """Training, scores and clause outputs at the largest sizes resolve_geometry accepts."""
+    """Training, scores and clause outputs at the largest sizes the persistent kernels take
+    and beyond them: more than 64 classes (one launch per sample) and more than 4096 patches."""
     case = dict(case)
     n, clauses = case.pop("n"), case.pop("clauses")
     kw = dict(number_of_clauses_per_class=clauses, T=20, s=3.0, seed=5, **case)
     tm = MultiClassTM(**kw)
     ref = orc.OracleTM(clauses, 20, 3.0, kw["dim"], kw["n_classes"],
-                       **{k: v for k, v in kw.items() if k in ("patch_dim", "number_of_ta_states", "seed")})
+                       **{k: v for k, v in kw.items() if k in ("patch_dim", "number_of_ta_states", "seed", "coalesced")})
     rng = np.random.default_rng(17)
     X = (rng.random((n, int(np.prod(kw["dim"])))) < 0.5).astype(np.uint32)
     y = rng.integers(0, kw["n_classes"], size=n).astype(np.uint32)
@@ -342,6 +353,8 @@ def test_supported_limits(case):
         upd = ref.fit_encoded(encX, ref.encode_y_multiclass(y))
         assert tm.stats()["last_fit_updates"] == upd
         assert_state_equal(tm, ref, f"epoch {epoch}")
+        if kw["n_classes"] > 64:
+            assert tm.stats()["train_kind"] == 4
     np.testing.assert_array_equal(tm.score(encX, is_X_encoded=True), ref.score(encX))
     np.testing.assert_array_equal(tm.transform(encX, is_X_encoded=True), ref.transform(encX))
     ref_pw = ref.transform(encX[:2], patchwise=True)

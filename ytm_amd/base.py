@@ -222,8 +222,8 @@ class BaseTM:
         tm._skip_gpu_init = True
         tm.__init__(*args, **kwargs)
         params = tm._params()
-        if not tm.coalesced:  # clause banks train with built-in kernels (train_kind 4)
-            return []
+        if not tm.coalesced or tm.number_of_outputs > 64:
+            return []  # clause banks and more than 64 classes: built-in kernels, a launch per sample (train_kind 4)
         P = tm.number_of_patches
         kinds = [0, 1] if P == 1 else ([0, 2] if (P + 31) // 32 <= 64 else [2])
         for kind in kinds:

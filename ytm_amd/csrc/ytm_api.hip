@@ -85,11 +85,15 @@ int ceil_log2(int64_t x) {
   return b;
 }
 
+// Classes of a model: the per-sample training kernel keeps three int64/double/int values
+// per class in LDS (step_lds_bytes), 80 KiB at this bound.
+constexpr int kMaxClasses = 4096;
+
 // Geometry of src/cutm/base.py:94-121 plus the bit-plane encoding of the TA states.
 int resolve_geometry(const ytm_params& p, Geom* out) {
   Geom g{};
   if (p.clauses < 1 || p.classes < 1) return fail(YTM_EINVAL, "clauses and classes must be >= 1");
-  if (p.classes > 64) return fail(YTM_EINVAL, "at most 64 classes are supported");
+  if (p.classes > kMaxClasses) return fail(YTM_EINVAL, "at most 4096 classes are supported");
   if (p.dim0 < 1 || p.dim1 < 1 || p.dim2 < 1) return fail(YTM_EINVAL, "dim entries must be >= 1");
   if (p.patch_dim0 < 1 || p.patch_dim1 < 1 || p.patch_dim0 > p.dim0 || p.patch_dim1 > p.dim1)
     return fail(YTM_EINVAL, "patch_dim must lie within dim");
@@ -107,7 +111,6 @@ int resolve_geometry(const ytm_params& p, Geom* out) {
   g.W = (g.L - 1) / 32 + 1;
   g.P = (int64_t)(p.dim0 - p.patch_dim0 + 1) * (p.dim1 - p.patch_dim1 + 1);
   g.F = (int64_t)p.dim0 * p.dim1 * p.dim2;
-  if (g.P > 64 * 64) return fail(YTM_EINVAL, "at most 4096 patches are supported");
   if (g.K * g.W * 6 >= ((int64_t)1 << 32)) return fail(YTM_EINVAL, "classes * literal words too large");
   if (!p.encode_loc && g.P > 1) {
     // kernel.cu:101-121 writes the thermometer bits even without ENCODE_LOC; the result is
@@ -333,20 +336,26 @@ ytm::TrainKind choose_train_kind(Geom* g, int cpw, bool force_global) {
   return kind;
 }
 
-// fit() of a clause-bank model (coalesced=False): one ordinary launch per sample plus one
-// (launch_bank_step), no persistent kernel and no wait between workgroups.  Slot memory:
-// three class-sum rows [3][64] int64, then sel [C] and ninc [C].
-int fit_banks(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count, const uint32_t* drop,
+// Models that train one sample per ordinary launch (launch_step) instead of on a
+// persistent kernel: clause banks (coalesced=False) and models of more than 64 classes
+// (the persistent kernels keep a class per lane).
+bool per_sample_training(const Geom& g) { return !g.coalesced || g.K > 64; }
+
+// fit() with one ordinary launch per sample plus one (launch_step), no persistent kernel
+// and no wait between workgroups: per_sample_training models, and models whose persistent
+// grid does not fit the device.  Slot memory: three class-sum rows [3][K] int64, then sel
+// [C] and ninc [C].
+int fit_steps(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count, const uint32_t* drop,
               const float* inject) {
   const Geom& g = m->g;
   const bool inj = inject != nullptr;
   const int64_t block = g.C * g.P + 2 * g.C * g.K + g.C * g.K * g.L;
   int64_t chunk = count;  // samples per copy of the injected blocks (<= 1 GiB)
   if (inj) chunk = std::min<int64_t>(chunk, std::max<int64_t>(1, ((int64_t)1 << 30) / (block * 4)));
-  int rc = ensure_slots(m, (size_t)(3 * 64 * 8 + g.C * 8));
+  int rc = ensure_slots(m, (size_t)(3 * g.K * 8 + g.C * 8));
   if (rc) return rc;
   long long* sums = (long long*)m->d_slots;
-  int* d_sel = (int*)(sums + 3 * 64);
+  int* d_sel = (int*)(sums + 3 * g.K);
   int* d_ninc = d_sel + g.C;
   uint32_t* d_drop = nullptr;
   float* d_inj = nullptr;
@@ -402,8 +411,8 @@ int fit_banks(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count,
     a.N = (int)n;
     a.g = g;
     BANK_TRY(hipEventRecord(m->ev0, m->stream));
-    BANK_TRY(ytm::launch_fill_u64((unsigned long long*)sums, 3 * 64, m->stream));
-    for (int64_t i = 0; i <= n; ++i) BANK_TRY(ytm::launch_bank_step(a, (int)i, sums, d_sel, d_ninc, inj, m->stream));
+    BANK_TRY(ytm::launch_fill_u64((unsigned long long*)sums, 3 * g.K, m->stream));
+    for (int64_t i = 0; i <= n; ++i) BANK_TRY(ytm::launch_step(a, (int)i, sums, d_sel, d_ninc, inj, m->stream));
     BANK_TRY(hipEventRecord(m->ev1, m->stream));
     BANK_TRY(hipEventSynchronize(m->ev1));
     float ms = 0.0f;
@@ -421,7 +430,7 @@ int fit_banks(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count,
   m->stats.last_fit_evaluations = (uint64_t)count;
   for (int j = 0; j < 3; ++j) m->stats.last_fit_draws[j] = 0;
   m->stats.last_fit_wait_frac = 0.0;
-  m->stats.train_kind = (int32_t)ytm::TrainKind::kBanks;
+  m->stats.train_kind = (int32_t)ytm::TrainKind::kSteps;
   m->stats.train_specialised = 0;
   m->stats.train_workgroups = (int32_t)std::min<int64_t>((g.C * 64 + 255) / 256, 65536);  // per launch
   m->stats.step += (uint64_t)count;
@@ -511,7 +520,7 @@ void ytm_destroy(ytm_model* m) {
 int ytm_load_train_kernels(ytm_model* m, int32_t kinds[4], int32_t* n_kinds) {
   if (!m || !kinds || !n_kinds) return fail(YTM_EINVAL, "null argument");
   *n_kinds = 0;
-  if (!m->g.coalesced || !ytm::jit_enabled()) return YTM_OK;  // built-in kernels only
+  if (per_sample_training(m->g) || !ytm::jit_enabled()) return YTM_OK;  // built-in kernels only
   const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
   const bool global = force_global && std::atoi(force_global) > 0;
   auto load = [&](const Geom& g, ytm::TrainKind kind) {
@@ -536,8 +545,9 @@ int ytm_compile_train_kernel(const ytm_params* params, int train_kind, int injec
   Geom model;
   int rc = resolve_geometry(*params, &model);
   if (rc) return rc;
-  if (!model.coalesced)
-    return fail(YTM_EINVAL, "clause banks (coalesced=False) train with built-in kernels; none is compiled per model");
+  if (per_sample_training(model))
+    return fail(YTM_EINVAL, "clause banks (coalesced=False) and models of more than 64 classes train with built-in "
+                            "kernels, one launch per sample; none is compiled per model");
   if (train_kind == 3) {
     Geom gs;
     if (injected || !stream_shape(model, compute_units > 0 ? compute_units : 256, &gs))
@@ -732,7 +742,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   m->stats.last_fit_kernel_ms = 0.0;
   m->stats.last_fit_launches = 0;
   if (count == 0) return YTM_OK;
-  if (!m->g.coalesced) return fit_banks(m, ds, first, count, drop, inject);
+  if (per_sample_training(m->g)) return fit_steps(m, ds, first, count, drop, inject);
   const bool inj = inject != nullptr;
   const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
   const bool global = force_global && std::atoi(force_global) > 0;
@@ -773,8 +783,9 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
     HIP_TRY(ytm::jit_occupancy(jit_fn, g.threads, lds, &bpc));
   else
     HIP_TRY(ytm::train_occupancy(kind, inj, lds, &bpc));
-  if ((int64_t)bpc * m->cus < grid)
-    return fail(YTM_EINVAL, "training grid does not fit co-resident on the device");
+  // a persistent grid that cannot be co-resident (its LDS, e.g. thresholds for very many
+  // patches) trains one sample per launch instead
+  if ((int64_t)bpc * m->cus < grid) return fit_steps(m, ds, first, count, drop, inject);
   m->stats.train_workgroups = grid;
 
   // Per-launch sample count: bounded by the class-sum slot memory (<= 256 MiB) and, in
@@ -936,8 +947,11 @@ struct ScorePlan {
 
 ScorePlan score_plan(const Geom& g, bool has_xt) {
   ScorePlan p{};
-  const size_t lm_bytes = has_xt ? ytm::score_lists_bytes(g) : 0;
-  const size_t wide_bytes = lm_bytes ? 0 : ytm::score_wide_bytes(g);
+  // the list-based and tiled scorers keep a class per lane: more than 64 classes take
+  // launch_score's class-sum kernel
+  const bool few = g.K <= 64;
+  const size_t lm_bytes = has_xt && few ? ytm::score_lists_bytes(g) : 0;
+  const size_t wide_bytes = lm_bytes || !few ? 0 : ytm::score_wide_bytes(g);
   p.lists_bytes = lm_bytes ? lm_bytes : wide_bytes;
   p.wide = wide_bytes > 0;
   p.chunks = p.lists_bytes ? 0 : ytm::score_tile_chunks(g);

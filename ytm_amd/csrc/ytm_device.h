@@ -13,7 +13,7 @@
 namespace ytm {
 
 constexpr int kWave = 64;
-constexpr int kMaxPlanes = 16;
+constexpr int kMaxPlanes = 32;  // every int32 number_of_ta_states fits (np <= 31)
 
 constexpr uint32_t TAG_SEL = 1;   // reservoir draw of the r-th firing patch
 constexpr uint32_t TAG_CK = 2;    // per (clause, class): Q-skip draw, update draw
@@ -63,7 +63,7 @@ __device__ __forceinline__ float uniform_from_word(uint32_t z) {
 // ---------------------------------------------------------------- bit-sliced TA state
 // Mask of the 32 lanes whose value (planes pl[0..np)) is < cst.  cst >= 2^np: all.
 __device__ __forceinline__ uint32_t planes_lt(const uint32_t* pl, int np, uint32_t cst) {
-  if (cst >> np) return 0xFFFFFFFFu;
+  if (np < 32 && (cst >> np)) return 0xFFFFFFFFu;
   uint32_t lt = 0u, eq = 0xFFFFFFFFu;
 #pragma unroll
   for (int j = kMaxPlanes - 1; j >= 0; --j) {

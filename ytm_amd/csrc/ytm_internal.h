@@ -83,15 +83,17 @@ constexpr size_t kResidentLdsLimit = 150 * 1024;
 // Training kernel variants: clause state resident in LDS (one patch), or kept in global
 // memory (one patch / several patches); kStream: one patch, clause state resident in LDS,
 // class sums of the samples ahead exchanged speculatively (train_stream_body).
-// kBanks: clause banks (coalesced=False), one ordinary launch per sample (launch_bank_step).
-enum class TrainKind { kResident, kGlobalVanilla, kGlobalConv, kStream, kBanks };
+// kSteps: one ordinary launch per sample (launch_step): clause banks (coalesced=False), more
+// than 64 classes, or a grid whose state does not fit.
+enum class TrainKind { kResident, kGlobalVanilla, kGlobalConv, kStream, kSteps };
 hipError_t train_occupancy(TrainKind kind, bool inject, size_t lds_bytes, int* blocks_per_cu);
 hipError_t launch_train(const TrainArgs& a, int grid, size_t lds_bytes, TrainKind kind, bool inject, hipStream_t s);
-// Launch i = 0 .. a.N of a clause-bank model's fit over a.N samples: the feedback of sample
-// i-1 and the evaluation of sample i; rows [3][64] int64 class sums (zero before launch 0);
-// sel / ninc hold the clauses' selected patches and include counts from one launch to the next.
-hipError_t launch_bank_step(const TrainArgs& a, int i, long long* rows, int* sel, int* ninc, bool inject,
-                            hipStream_t s);
+// Launch i = 0 .. a.N of a per-sample fit over a.N samples: the feedback of sample i-1 and
+// the evaluation of sample i; rows [3][K] int64 class sums (zero before launch 0); sel /
+// ninc hold the clauses' selected patches and include counts from one launch to the next.
+// Its dynamic LDS is step_lds_bytes(g) (partial sums, probabilities and targets per class).
+hipError_t launch_step(const TrainArgs& a, int i, long long* rows, int* sel, int* ninc, bool inject, hipStream_t s);
+size_t step_lds_bytes(const Geom& g);
 size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g);
 // LDS of the streaming kernel for a workgroup of `threads` threads.
 size_t stream_lds_bytes(const Geom& g, int threads);

@@ -225,6 +225,41 @@ __global__ __launch_bounds__(256) void score_kernel(const uint32_t* __restrict__
   }
 }
 
+// More than 64 classes: as score_kernel, but a firing clause's weights go into the block's
+// LDS sums [K] (int64 atomics, 64 classes per wave step), which the block adds into acc at
+// the end of its chunk.
+template <bool VANILLA>
+__global__ __launch_bounds__(256) void score_classes_kernel(const uint32_t* __restrict__ planes,
+                                                            const int32_t* __restrict__ ninc,
+                                                            const float* __restrict__ w,
+                                                            const uint32_t* __restrict__ X, int64_t N, Geom g,
+                                                            long long* __restrict__ acc) {
+  extern __shared__ long long s_sum[];  // [K]
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  const int64_t nch = (g.C + kScoreChunk - 1) / kScoreChunk;
+  for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
+    const int64_t e = blk / nch, ch = blk % nch;
+    const int64_t c0 = ch * kScoreChunk;
+    const int64_t c1 = c0 + kScoreChunk < g.C ? c0 + kScoreChunk : g.C;
+    const uint32_t* xe = X + e * g.P * g.W;
+    __syncthreads();  // the previous chunk's sums are flushed
+    for (int64_t k = threadIdx.x; k < g.K; k += blockDim.x) s_sum[k] = 0;
+    __syncthreads();
+    for (int64_t c = c0 + wave; c < c1; c += nw) {
+      if (ninc[c] == 0) continue;  // empty clauses do not vote (kernel.cu:328)
+      if (clause_fires_any<VANILLA>(planes + (c * g.np + g.np - 1) * g.W, xe, g))
+        for (int64_t k = lane; k < g.K; k += kWave) {
+          const long long v = (long long)w[c * g.K + k];
+          if (v != 0) atomicAdd((unsigned long long*)&s_sum[k], (unsigned long long)v);
+        }
+    }
+    __syncthreads();
+    for (int64_t k = threadIdx.x; k < g.K; k += blockDim.x)
+      if (s_sum[k] != 0) atomicAdd((unsigned long long*)&acc[e * g.K + k], (unsigned long long)s_sum[k]);
+  }
+}
+
 // One patch: lanes are samples.  A block takes a tile of 64 samples (staged transposed in
 // LDS, [W][64], so that lane e reads word w of its own sample) and a chunk of clauses; each
 // wave walks its clauses, reading a clause's mask words once and skipping the zero ones with
@@ -721,40 +756,46 @@ __global__ __launch_bounds__(kTrainThreads) void train_resident_kernel(TrainArgs
 
 __global__ __launch_bounds__(kTrainThreads) void train_stream_kernel(TrainArgs a) { train_stream_body(a, a.g); }
 
-// Clause banks (coalesced=False: clause c votes for and learns only its bank's class
-// c / per_bank, kernel.cu:306-312,563-565) train with one ordinary launch per sample, a wave
-// per clause at a time.  Launch i runs, for each clause, the feedback of sample i-1
-// (clause_update, kernel.cu:531-613, from the class totals the previous launch completed)
-// and then the evaluation of sample i (fast_eval and select_active, kernel.cu:255-316),
-// which needs only the clause's own state: its selected patch and include count go to
-// sel / ninc, its patch weight is counted and its bank vote added into sample i's class-sum
-// row (int64).  The launch boundary orders the samples, so no workgroup ever waits on
-// another.  Rows cycle through three: launch i reads row (i-1) % 3, adds into row i % 3 and
-// clears row (i+1) % 3, which the previous launch read and the next one adds into.  Launch 0
-// only evaluates and launch N only applies feedback.
+// Per-sample training (one ordinary launch per sample), for clause banks (coalesced=False:
+// clause c votes for and learns only its bank's class c / per_bank, kernel.cu:306-312,
+// 563-565) and for models the persistent kernels do not take (more than 64 classes, or a
+// grid whose state does not fit), a wave per clause at a time.  Launch i runs, for each
+// clause, the feedback of sample i-1 (clause_update, kernel.cu:531-613, from the class
+// totals the previous launch completed; with more than 64 classes decided and applied 64
+// classes at a time, in increasing k, which is the reference's order: the decisions read
+// only the evaluation's results) and then the evaluation of sample i (fast_eval and
+// select_active, kernel.cu:255-316), which needs only the clause's own state: its selected
+// patch and include count go to sel / ninc, its patch weight is counted and its votes added
+// into sample i's class-sum row (int64).  The launch boundary orders the samples, so no
+// workgroup ever waits on another.  Rows [3][K] cycle: launch i reads row (i-1) % 3, adds
+// into row i % 3 and clears row (i+1) % 3, which the previous launch read and the next one
+// adds into.  Launch 0 only evaluates and launch N only applies feedback.  Dynamic LDS:
+// partial sums int64 [K], probabilities double [K], targets int [K] (step_lds_bytes).
 template <bool ONE_PATCH, bool INJECT>
-__global__ __launch_bounds__(256) void bank_step_kernel(TrainArgs a, int i, long long* __restrict__ rows,
-                                                        int* __restrict__ sel, int* __restrict__ ninc) {
+__global__ __launch_bounds__(256) void step_kernel(TrainArgs a, int i, long long* __restrict__ rows,
+                                                   int* __restrict__ sel, int* __restrict__ ninc) {
   const Geom& g = a.g;
-  __shared__ long long s_part[64];
-  __shared__ int s_tgt[64];
-  __shared__ double s_prob[64];
+  extern __shared__ __attribute__((aligned(16))) long long step_lds[];
+  long long* s_part = step_lds;                   // [K]
+  double* s_prob = (double*)(s_part + g.K);       // [K]
+  int* s_tgt = (int*)(s_prob + g.K);              // [K]
   __shared__ unsigned long long s_upd;
   const int lane = lane_id();
   const bool fb = i > 0, ev = i < a.N;
-  const long long* sums_prev = rows + ((i + 2) % 3) * 64;
-  long long* sums_cur = rows + (i % 3) * 64;
-  long long* sums_next = rows + ((i + 1) % 3) * 64;
-  if (threadIdx.x < 64) s_part[threadIdx.x] = 0;
+  const long long* sums_prev = rows + ((i + 2) % 3) * g.K;
+  long long* sums_cur = rows + (i % 3) * g.K;
+  long long* sums_next = rows + ((i + 1) % 3) * g.K;
+  for (int64_t k = threadIdx.x; k < g.K; k += blockDim.x) {
+    s_part[k] = 0;
+    if (fb) class_targets(g, (int)k, sums_prev[k] + (long long)a.bias[k], a.Y + (int64_t)(i - 1) * g.K, s_tgt, s_prob);
+    if (blockIdx.x == 0) sums_next[k] = 0;
+  }
   if (threadIdx.x == 0) s_upd = 0ull;
-  if (fb && threadIdx.x < g.K)
-    class_targets(g, (int)threadIdx.x, sums_prev[threadIdx.x] + (long long)a.bias[threadIdx.x],
-                  a.Y + (int64_t)(i - 1) * g.K, s_tgt, s_prob);
-  if (blockIdx.x == 0 && threadIdx.x < 64) sums_next[threadIdx.x] = 0;
   __syncthreads();
   if (fb && blockIdx.x == 0 && threadIdx.x < kWave) {  // samples where some class may update
-    const bool any = __ballot(lane < g.K && s_prob[lane < g.K ? lane : 0] > 0.0) != 0ull;
-    if (lane == 0 && any) atomicAdd(&a.counters[12], 1ull);
+    bool any = false;
+    for (int64_t k = lane; k < g.K; k += kWave) any = any || s_prob[k] > 0.0;
+    if (lane == 0 && __any(any)) atomicAdd(&a.counters[12], 1ull);
   }
   const int64_t wave0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const int64_t nwaves = (int64_t)gridDim.x * blockDim.x / kWave;
@@ -764,13 +805,20 @@ __global__ __launch_bounds__(256) void bank_step_kernel(TrainArgs a, int i, long
   const float* inj = INJECT && ev ? a.inject + (int64_t)i * a.inject_block : nullptr;
   const uint32_t* xp = a.X + (int64_t)(fb ? i - 1 : 0) * g.P * g.W;
   const uint32_t* xe = a.X + (int64_t)(ev ? i : 0) * g.P * g.W;
+  const int64_t kspan = g.coalesced ? g.K : 1;  // classes a clause learns, 64 per decision
   for (int64_t c = wave0; c < g.C; c += nwaves) {
     if (fb && a.drop[c] != 1u) {  // a dropped clause gets no feedback (kernel.cu:555)
       const int sl = sel[c];
-      const FbOps ops = decide<INJECT>(a, g, injp, c, tp, sl, ninc[c], s_tgt, s_prob, a.weights + c * g.K, nullptr,
-                                       nullptr);
-      if ((ops.m1a | ops.m1b | ops.m2) != 0ull) {
-        apply_ops<INJECT>(a, g, injp, c, tp, sl, ops, a.planes + c * cw, xp, nullptr);
+      bool updated = false;
+      for (int64_t kc = 0; kc < kspan; kc += kWave) {
+        const FbOps ops = decide<INJECT>(a, g, injp, c, tp, sl, ninc[c], s_tgt, s_prob, a.weights + c * g.K, nullptr,
+                                         nullptr, false, kc);
+        if ((ops.m1a | ops.m1b | ops.m2) != 0ull) {
+          apply_ops<INJECT>(a, g, injp, c, tp, sl, ops, a.planes + c * cw, xp, nullptr, nullptr, 0, -1, kc);
+          updated = true;
+        }
+      }
+      if (updated) {
         if (lane == 0) atomicAdd(&s_upd, 1ull);
         __threadfence();  // the new planes (every lane's words) before the evaluation reads them
       }
@@ -782,17 +830,25 @@ __global__ __launch_bounds__(256) void bank_step_kernel(TrainArgs a, int i, long
       if (lane == 0) {
         sel[c] = sl;
         ninc[c] = n;
-        if (sl >= 0) {
+        if (sl >= 0) a.patch_w[c * g.P + sl] += 1;
+      }
+      if (sl >= 0) {
+        if (g.coalesced) {
+          for (int64_t k = lane; k < g.K; k += kWave) {
+            const long long v = (long long)a.weights[c * g.K + k];
+            if (v != 0) atomicAdd((unsigned long long*)&s_part[k], (unsigned long long)v);
+          }
+        } else if (lane == 0) {
           const int64_t k = c / g.per_bank;
-          a.patch_w[c * g.P + sl] += 1;
           atomicAdd((unsigned long long*)&s_part[k], (unsigned long long)(long long)a.weights[c * g.K + k]);
         }
       }
     }
   }
   __syncthreads();
-  if (ev && threadIdx.x < g.K && s_part[threadIdx.x] != 0)
-    atomicAdd((unsigned long long*)&sums_cur[threadIdx.x], (unsigned long long)s_part[threadIdx.x]);
+  if (ev)
+    for (int64_t k = threadIdx.x; k < g.K; k += blockDim.x)
+      if (s_part[k] != 0) atomicAdd((unsigned long long*)&sums_cur[k], (unsigned long long)s_part[k]);
   if (threadIdx.x == 0 && s_upd) atomicAdd(&a.counters[0], s_upd);
 }
 
@@ -1087,6 +1143,14 @@ hipError_t launch_score(const uint32_t* planes, const int32_t* ninc, const float
   }
   const int64_t blocks = N * ((g.C + kScoreChunk - 1) / kScoreChunk);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
+  if (g.K > kWave) {
+    const size_t lds = (size_t)g.K * 8;
+    if (g.P == 1)
+      score_classes_kernel<true><<<grid, 256, lds, s>>>(planes, ninc, w, X, N, g, acc);
+    else
+      score_classes_kernel<false><<<grid, 256, lds, s>>>(planes, ninc, w, X, N, g, acc);
+    return hipGetLastError();
+  }
   if (g.P == 1)
     score_kernel<true><<<grid, 256, 0, s>>>(planes, ninc, w, X, N, g, acc);
   else
@@ -1215,18 +1279,20 @@ hipError_t launch_train(const TrainArgs& a, int grid, size_t lds_bytes, TrainKin
                                     (unsigned)lds_bytes, s);
 }
 
-hipError_t launch_bank_step(const TrainArgs& a, int i, long long* rows, int* sel, int* ninc, bool inject,
-                            hipStream_t s) {
+size_t step_lds_bytes(const Geom& g) { return (size_t)g.K * (8 + 8 + 4); }
+
+hipError_t launch_step(const TrainArgs& a, int i, long long* rows, int* sel, int* ninc, bool inject, hipStream_t s) {
   const int grid = grid_for(a.g.C * kWave, 256);
   const bool one = a.g.P == 1;
+  const size_t lds = step_lds_bytes(a.g);
   if (one && inject)
-    bank_step_kernel<true, true><<<grid, 256, 0, s>>>(a, i, rows, sel, ninc);
+    step_kernel<true, true><<<grid, 256, lds, s>>>(a, i, rows, sel, ninc);
   else if (one)
-    bank_step_kernel<true, false><<<grid, 256, 0, s>>>(a, i, rows, sel, ninc);
+    step_kernel<true, false><<<grid, 256, lds, s>>>(a, i, rows, sel, ninc);
   else if (inject)
-    bank_step_kernel<false, true><<<grid, 256, 0, s>>>(a, i, rows, sel, ninc);
+    step_kernel<false, true><<<grid, 256, lds, s>>>(a, i, rows, sel, ninc);
   else
-    bank_step_kernel<false, false><<<grid, 256, 0, s>>>(a, i, rows, sel, ninc);
+    step_kernel<false, false><<<grid, 256, lds, s>>>(a, i, rows, sel, ninc);
   return hipGetLastError();
 }
 

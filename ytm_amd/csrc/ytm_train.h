@@ -635,11 +635,8 @@ __device__ int eval_select(const TrainArgs& a, const Geom& g, const float* inj, 
     const int ninc = exact_count ? wave_sum_i32(cnt) : (__any(any != 0u) ? 1 : 0);
     *ninc_out = ninc;
     if (dropped) return -1;
-    // Firing bitmap: lane q keeps bits of patches [64q, 64q+64).
-    unsigned long long myfire = 0ull;
-    int R = 0;
-    const int nch = (int)((g.P + kWave - 1) / kWave);
-    for (int ch = 0; ch < nch; ++ch) {
+    // Firing patches of chunk ch, lane q: patch 64 ch + q.
+    auto chunk_fire = [&](int ch) -> unsigned long long {
       const int64_t p = (int64_t)ch * kWave + lane;
       bool ok = p < g.P;
       if (ok && ninc != 0) {
@@ -650,13 +647,36 @@ __device__ int eval_select(const TrainArgs& a, const Geom& g, const float* inj, 
             break;
           }
       }
-      const unsigned long long b = __ballot(ok);
+      return __ballot(ok);
+    };
+    // Firing bitmap: lane q keeps bits of patches [64q, 64q+64) (the first 64 chunks).
+    unsigned long long myfire = 0ull;
+    int R = 0;
+    const int nch = (int)((g.P + kWave - 1) / kWave);
+    for (int ch = 0; ch < nch; ++ch) {
+      const unsigned long long b = chunk_fire(ch);
       if (lane == ch) myfire = b;
       R += __popcll(b);
     }
     if (R == 0) return -1;
     const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R, a.inv_rank);
     if (best == 0) return -1;
+    if (nch > kWave) {
+      // more than 4096 patches: the chunks again, up to the one holding the best-th firing
+      // patch
+      int before = 0;
+      for (int ch = 0; ch < nch; ++ch) {
+        const unsigned long long b = chunk_fire(ch);
+        const int pc = __popcll(b);
+        if (before + pc >= best) {
+          unsigned long long v = b;
+          for (int q = 1; q < best - before; ++q) v &= v - 1ull;
+          return ch * kWave + __ffsll((long long)v) - 1;
+        }
+        before += pc;
+      }
+      return -1;  // not reached: best <= R
+    }
     // Patch of the best-th set bit of the firing bitmap.
     const int pc = lane < nch ? __popcll(myfire) : 0;
     const int incl = wave_inclusive_scan(pc);
@@ -683,13 +703,14 @@ struct FbOps {
 // literal updates are left to apply_ops.  Wave-uniform result.  Every input is loaded
 // before any decision is taken and the decisions are selects, so the loads overlap
 // instead of forming a chain of dependent LDS round trips.
+// kc: with more than 64 classes (coalesced), the first of the 64 classes decided here.
 template <bool INJECT, bool PRE = false>
 __device__ FbOps decide(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, int sel, int ninc,
                         const int* s_tgt, const double* s_prob, float* wrow, const float* pre_uq,
-                        const float* pre_uu, bool dropped = false) {
+                        const float* pre_uu, bool dropped = false, int64_t kc = 0) {
   const int lane = lane_id();
-  const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
-  const int kn = g.coalesced ? (int)g.K : 1;
+  const int64_t kb = g.coalesced ? kc : c / g.per_bank;
+  const int kn = g.coalesced ? (int)(g.K - kc < kWave ? g.K - kc : kWave) : 1;
   const int64_t k = kb + (lane < kn ? lane : 0);  // idle lanes read class kb's inputs and discard them
   const bool act = lane < kn && !dropped;        // a dropped clause gets no feedback (kernel.cu:555)
   const int tgt = s_tgt[k];
@@ -788,14 +809,15 @@ __device__ __forceinline__ PairOps decide_pair(const Geom& g, const float* inj, 
 // Literal updates of one clause for the feedback decided in ops, applied class by class
 // in increasing k to the clause's planes (cplanes, stride W).  pre, when given, holds the
 // first kPreGroups plane groups of the literal draws of every Type Ia/Ib class, in the
-// order of those classes: [op][W][kPreGroups][4].
+// order of those classes: [op][W][kPreGroups][4].  kc: as in decide (bit b of ops is class
+// kc + b of a coalesced model).
 template <bool INJECT>
 __device__ void apply_ops(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, int sel, FbOps ops,
                           uint32_t* cplanes, const uint32_t* xe, const uint32_t* pre, uint32_t* top_copy = nullptr,
-                          int64_t wb_first = 0, int64_t wb_end = -1) {
+                          int64_t wb_first = 0, int64_t wb_end = -1, int64_t kc = 0) {
   // words [wb_first, wb_end) of the clause (wb_first a multiple of 64; wb_end < 0: to W)
   const int lane = lane_id();
-  const int64_t kb = g.coalesced ? 0 : c / g.per_bank;
+  const int64_t kb = g.coalesced ? kc : c / g.per_bank;
   const bool o = sel >= 0;
   const uint32_t* xsel = o ? xe + (int64_t)sel * g.W : nullptr;
   const int np = g.np;

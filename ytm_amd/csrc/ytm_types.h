@@ -16,7 +16,7 @@ using __hip_internal::uint64_t;
 namespace ytm {
 
 constexpr int kTrainThreads = 512;  // workgroup size of the built-in training kernels
-constexpr int kMaxPlanesHost = 16;  // must equal kMaxPlanes of ytm_device.h
+constexpr int kMaxPlanesHost = 32;  // must equal kMaxPlanes of ytm_device.h
 
 // Resolved model geometry and hyperparameters.  Listed once (X-macro) so that host code
 // can print a constexpr initializer in declaration order for a specialised compile.
