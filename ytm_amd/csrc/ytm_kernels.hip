@@ -1047,13 +1047,21 @@ size_t score_lists_bytes(const Geom& g) {
 
 size_t score_wide_bytes(const Geom& g) { return score_wide_fits(g) ? lists_scratch_bytes(g) : 0; }
 
-// Literal order from the batch, then the lists in that order.
+// Literal order from the batch, then the lists in that order: several patches (XT given),
+// whose walks end at the first AND over all patches that is empty (config 4: 149K -> 244K
+// samples/s with the two-half test).  One-patch lists (wide_kernel, lanes = clauses over a
+// tile of 32 samples) stay in literal index order, which measured faster there (config 2:
+// 149M against 135M samples/s).  YTM_LIST_ORDER=0: index order everywhere.
 static hipError_t build_lists(const uint32_t* planes, const uint32_t* X, const uint32_t* XT, int64_t N,
                               const Geom& g, const ListScratch& ls, hipStream_t s) {
-  hipError_t e = launch_literal_order(X, XT, N, g, ls.order, s);
-  if (e != hipSuccess) return e;
-  build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, ls.order, ls.lists,
-                                                                  ls.nlit);
+  const char* env = std::getenv("YTM_LIST_ORDER");
+  const bool ordered = XT != nullptr && !(env && std::atoi(env) == 0);
+  if (ordered) {
+    hipError_t e = launch_literal_order(X, XT, N, g, ls.order, s);
+    if (e != hipSuccess) return e;
+  }
+  build_lists_kernel<<<grid_for(g.C * kWave, 256), 256, 0, s>>>(planes, g, kScoreListCap, ordered ? ls.order : nullptr,
+                                                                  ls.lists, ls.nlit);
   return hipGetLastError();
 }
 
