@@ -85,8 +85,9 @@ typedef struct ytm_stats {
                                     waiting for the per-sample class sums */
     int32_t train_kind;          /* 0 = clause state resident in LDS, 1 = global (one
                                     patch), 2 = global (several patches), 3 = resident and
-                                    streaming (one patch), 4 = clause banks (coalesced=0):
-                                    one ordinary launch per sample */
+                                    streaming (one patch), 4 = one ordinary launch per
+                                    sample: clause banks (coalesced=0), more than 64
+                                    classes, or a persistent grid that does not fit */
     int32_t train_specialised;   /* 1 when the last fit ran a training kernel compiled at run
                                     time for this model's geometry (hipRTC), 0 when it ran the
                                     built-in kernel (YTM_JIT=0, or the compile was unavailable) */
@@ -127,7 +128,11 @@ int ytm_shutdown(void);
 
 /* Model lifetime.  Replaces BaseTM._gpu_init / _reset_clauses / _reset_weights
  * (src/cutm/base.py:128-222; kernel.cu:46-73 init_weights): TA states start at
- * number_of_ta_states/2, weights from the INIT random site, patch weights and bias 0. */
+ * number_of_ta_states/2, weights from the INIT random site, patch weights and bias 0.
+ * Geometry bounds: at most 4096 classes (the reference's kernels take any CLASSES; more
+ * than 64 train one sample per launch), any number of patches, any int32
+ * number_of_ta_states (up to 32 bit-planes), classes * literal words * 6 below 2^32 (the
+ * 32-bit literal-draw site index of the counter stream).  YTM_EINVAL otherwise. */
 int ytm_create(const ytm_params *params, ytm_model **out);
 void ytm_destroy(ytm_model *m);
 /* L, W (=number_of_literal_chunks), P (=number_of_patches), number of TA bit-planes. */
@@ -140,7 +145,8 @@ int ytm_set_seed(ytm_model *m, uint64_t seed);
  * MI355X), without touching a GPU.  train_kind as in ytm_stats (0 resident: one patch, or
  * several with ceil(P/32) <= 64; 1 global one patch; 2 global several patches; 3 streaming:
  * one patch, coalesced, counter stream only); injected != 0 for the injected-draw variant.
- * Clause-bank models (coalesced = 0) train with built-in kernels only: YTM_EINVAL.
+ * Clause-bank models (coalesced = 0) and models of more than 64 classes train with built-in
+ * kernels only (train_kind 4): YTM_EINVAL.
  * The counterpart of the per-model kernel compile in BaseTM.__init__
  * (src/cutm/base.py:129-159); ytm_fit compiles on first use anyway, so calling this is
  * optional (warm-up, or checking that the compiler is available).  YTM_EHIP with the
