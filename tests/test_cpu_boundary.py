@@ -149,9 +149,9 @@ def test_bench_profile_summaries(cfg):
     assert tr["bytes_per_launch"] > 0 and 0 < tr["hbm_gbs"] < bench.HBM_PEAK_GBS
     assert 0.0 <= ct["valu_busy"] <= 1.0 and 0.0 <= ct["lds_bank_conflict"] <= 1.0
     assert ct["valu_insts_per_sample"] > 0
-    for d in (tr, ct):
-        if "source_sha16" in d:
-            assert len(d["source_sha16"]) == 16 and int(d["source_sha16"], 16) >= 0
+    for d in (tr, ct):  # measured on the kernel sources of this tree
+        assert d["source_sha16"] == bench.kernel_source_hash()
+    assert tr["epochs"] == ct["epochs"] and tr["bytes_per_launch"] < tr["algorithmic_bytes_per_launch"] * 2
 
 
 def test_bench_reports_only_current_profiles(tmp_path, monkeypatch):
