@@ -1,7 +1,9 @@
-"""ytm_score_dataset_noalloc (the allocation-free scorer) against ytm_score_dataset.
+"""ytm_score_dataset_noalloc (the allocation-free scorer) against ytm_score_dataset and the
+C oracle.
 
 Both are called through the C-ABI on the same model and device-resident dataset; the
-allocation-free one writes into a caller-owned device buffer.  Two calls in a row, the
+allocation-free one writes into a caller-owned device buffer, and the oracle, loaded with
+the GPU model's state, scores the same samples.  Two calls in a row, the
 second on fewer samples, so a stale scratch array from the first call would show.  Every
 scoring kernel path is covered: wide one-patch clauses (literal lists), several patches
 (literal-major samples), narrow one-patch clauses (per-chunk sums, several passes over the
@@ -13,6 +15,7 @@ import numpy as np
 import pytest
 
 import workloads
+from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -82,12 +85,18 @@ def test_noalloc_matches_score_dataset(case):
         Xt = (rng.random((500, 40)) < 0.5).astype(np.uint32)
         sizes = (500, 120)
     encXt = tm.encode(Xt)
+    okw = dict(kw)
+    okw.pop("seed", None)
+    oracle = orc.OracleTM(okw.pop("number_of_clauses_per_class"), okw.pop("T"), okw.pop("s"), okw.pop("dim"),
+                          okw.pop("n_classes"), **okw)
+    oracle.load_state(tm.get_ta_state(), tm.get_weights(), tm.get_patch_weights(), tm.stats()["step"])
     for n in sizes:
         data = tm.device_data(encXt[:n], is_X_encoded=True)
         ref, got = score_both(tm, data, tm.number_of_outputs)
         data.release()
         np.testing.assert_array_equal(got, ref, err_msg=f"{case} n={n}")
         assert np.any(ref != 0), "a meaningful comparison needs non-zero class sums"
+        np.testing.assert_array_equal(got, oracle.score(encXt[:n]), err_msg=f"{case} n={n}: oracle")
     tm.release()
 
 
