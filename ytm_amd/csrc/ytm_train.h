@@ -952,6 +952,16 @@ __device__ __forceinline__ ClassFb class_fb(const Geom& g, long long S, int y) {
   return ClassFb{1 - 2 * (vclip > (float)y), ((double)y - (double)vclip) / (2.0 * (double)y)};
 }
 
+// class_fb(g, S, y).prob > 0.0 without the division: the quotient (y - vclip) / (2y) of two
+// exact doubles is positive exactly when numerator and denominator have the same sign and
+// the numerator is not zero; with y = 0 it is +inf (true) for y - vclip > 0, else -inf or NaN.
+__device__ __forceinline__ bool class_may_update(const Geom& g, long long S, int y) {
+  const float cs = (float)S;
+  const float vclip = ((double)cs > g.thresh) ? (float)g.thresh : (((double)cs < -g.thresh) ? (float)(-g.thresh) : cs);
+  const double d = (double)y - (double)vclip;
+  return y >= 0 ? d > 0.0 : d < 0.0;
+}
+
 // class_fb without the int64 -> float conversion and the division, for an integral
 // threshold 0 <= T < 2^24 and a target 0 < |y| < 2^28 (exact).  The clip is taken on the
 // integer sum: for such T, (float)S > T exactly when S > T, and |S| <= T converts exactly,
@@ -2616,7 +2626,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         bool fb = false;
         if (live) {
           const int y = s_yring[((j + q) & (D - 1)) * K + k];
-          fb = class_fb(g, S, y).prob > 0.0;
+          fb = class_may_update(g, S, y);  // class_fb(g, S, y).prob > 0
         }
         const unsigned long long fbm = __ballot(fb);
         const int qf = fbm ? (__ffsll((long long)fbm) - 1) / K : ncomp;  // first row with feedback
