@@ -362,6 +362,46 @@ def test_supported_limits(case):
     assert_packed_equal(tm.transform_patchwise(encX[:2], is_X_encoded=True, packed=True), ref_pw)
 
 
+@pytest.mark.parametrize("case", [
+    dict(dim=(12, 1, 1), n_classes=130, clauses=24, n=120),
+    dict(dim=(8, 8, 1), patch_dim=(3, 3), n_classes=66, clauses=16, n=30),
+])
+def test_many_classes_injected_and_multioutput(case):
+    """More than 64 classes on the per-sample path: injected draws (Q-skip, update and
+    literal draws indexed by class past 64, reservoir u = 1.0), then MultiOutputTM with 70
+    outputs, against the oracle."""
+    case = dict(case)
+    n, clauses = case.pop("n"), case.pop("clauses")
+    kw = dict(number_of_clauses_per_class=clauses, T=15, s=2.5, seed=9, **case)
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(clauses, 15, 2.5, kw["dim"], kw["n_classes"],
+                       **{k: v for k, v in kw.items() if k in ("patch_dim", "seed")})
+    rng = np.random.default_rng(31)
+    X = (rng.random((n, int(np.prod(kw["dim"])))) < 0.5).astype(np.uint32)
+    y = rng.integers(0, kw["n_classes"], size=n).astype(np.uint32)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    for epoch in range(2):
+        inj = rng.random(tm.random_stream_size(n)).astype(np.float32)
+        inj[::13] = 1.0
+        tm.fit(encX, y, is_X_encoded=True, random_stream=inj)
+        upd = ref.fit_encoded(encX, encY, inject=inj)
+        assert tm.stats()["train_kind"] == 4
+        assert tm.stats()["last_fit_updates"] == upd
+        assert_state_equal(tm, ref, f"injected epoch {epoch}")
+    np.testing.assert_array_equal(tm.score(encX, is_X_encoded=True), ref.score(encX))
+    # multi-output: 70 independent +-T targets
+    from ytm_amd import MultiOutputTM
+    mo = MultiOutputTM(**dict(kw, n_classes=70))
+    refo = orc.OracleTM(clauses, 15, 2.5, kw["dim"], 70, **{k: v for k, v in kw.items() if k in ("patch_dim", "seed")})
+    Y = (rng.random((n, 70)) < 0.3).astype(np.uint32)
+    mo.fit(encX, Y, is_X_encoded=True)
+    upd = refo.fit_encoded(encX, np.where(Y == 1, 15, -15).astype(np.int32))
+    assert mo.stats()["last_fit_updates"] == upd
+    assert_state_equal(mo, refo, "multi-output")
+    np.testing.assert_array_equal(mo.score(encX, is_X_encoded=True), refo.score(encX))
+
+
 def test_fit_conv_lists_of_literal_indices():
     """Literal lists hold byte offsets into the literal-major sample only while those fit 16
     bits; with 696 literals over 29 patch words ((L-1) * 4 * 29 > 65535) they hold literal
