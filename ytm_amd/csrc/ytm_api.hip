@@ -309,7 +309,13 @@ bool stream_shape(const Geom& mg, int cus, Geom* out) {
   g.groups = 1;
   g.list_cap = 0;
   g.mask_lds = 0;
-  if (ytm::stream_lds_bytes(g, std::max(g.threads, ytm::kTrainThreads)) > ytm::kResidentLdsLimit) return false;
+  g.vote_table = 0;
+  const size_t base = ytm::stream_lds_bytes(g, std::max(g.threads, ytm::kTrainThreads));
+  if (base > ytm::kResidentLdsLimit) return false;
+  // class votes from nibble tables when they fit (YTM_STREAM_VOTE_TABLE=0 turns them off)
+  const char* vt_env = std::getenv("YTM_STREAM_VOTE_TABLE");
+  g.vote_table = g.K <= 16 && base + ytm::stream_vote_table_bytes(g) <= ytm::kResidentLdsLimit &&
+                 !(vt_env && std::atoi(vt_env) == 0);
   *out = g;
   return true;
 }

@@ -97,6 +97,8 @@ size_t step_lds_bytes(const Geom& g);
 size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g);
 // LDS of the streaming kernel for a workgroup of `threads` threads.
 size_t stream_lds_bytes(const Geom& g, int threads);
+// LDS of the streaming kernel's vote tables (Geom::vote_table).
+size_t stream_vote_table_bytes(const Geom& g);
 // Literal-draw slots the resident kernel precomputes per sample within an LDS budget.
 int train_rng_slots(int cpw, const Geom& g);
 

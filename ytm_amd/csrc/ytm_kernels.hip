@@ -1258,8 +1258,11 @@ size_t stream_lds_bytes(const Geom& g, int threads) {
   (void)threads;
   const size_t C = kStreamClauses, K = (size_t)g.K, Wp = (size_t)((g.W + 3) & ~(int64_t)3);
   return 3 * C * 8 + C * (size_t)g.np * (size_t)g.W * 4 + 2 * C * K * 4 + 6 * C * 4 + (size_t)kStreamDepth * K * 4 +
-         (size_t)kStreamDepth * Wp * 4 + K * C * 4 + Wp * C * 4;
+         (size_t)kStreamDepth * Wp * 4 + K * C * 4 + Wp * C * 4 + (g.vote_table ? stream_vote_table_bytes(g) : 0);
 }
+
+// the vote nibble tables [16][16][K] (16-bit) of train_stream_body
+size_t stream_vote_table_bytes(const Geom& g) { return (size_t)kStreamClauses / 4 * 16 * (size_t)g.K * 2; }
 
 static const void* train_fn(TrainKind kind, bool inject) {
   switch (kind) {

@@ -2470,6 +2470,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   __shared__ int s_wmax;                               // bound on |integer weight| of the own clauses
   __shared__ long long s_S[64];                        // class sums + bias of the stop sample
   __shared__ int s_ntask;
+  __shared__ int s_vdirty[64];                         // vote tables: nibble groups changed at a stop, per class
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int nwv = blockDim.x / kWave;
@@ -2500,6 +2501,19 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   int* s_wt_old = (int*)(s_nx + (int64_t)D * Wp);  // [K][64] integer weights before a stop
   uint4* s_maskT = (uint4*)(s_wt_old + K * kStreamClauses);
   const int64_t Wq = Wp / 4;
+  // g.vote_table: class votes from nibble tables [16][16][K] int16, entry (j, v, k) the sum
+  // of the integer weights of class k of the clauses 4j + b with bit b of v set; a
+  // selection mask then gives lane k its class's vote in 16 table reads.  Exact while every
+  // own |weight| is below 512 (an entry stays within +-2044), as the paired reduction.
+  short* s_vt = (short*)(s_maskT + Wq * kStreamClauses);
+  auto vt_entry = [&](int e) -> short {  // entry e = (j * 16 + v) * K + k, from s_wt
+    const int k = e % K, jv = e / K, j = jv >> 4, v = jv & 15;
+    int sum = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if ((v >> b) & 1) sum += s_wt[k * kStreamClauses + 4 * j + b];
+    return (short)sum;
+  };
   // word group w4 of clause idx's include mask (zero past W and past the own clauses)
   auto mask_quad = [&](int idx, int64_t w4) -> uint4 {
     const uint32_t* mt = s_planes + idx * cw + (int64_t)(g.np - 1) * g.W;
@@ -2523,6 +2537,9 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
     s_wt[(j % K) * kStreamClauses + j / K] = (int)w;
     atomicMax(&s_wmax, (int)w < 0 ? -(int)w : (int)w);
   }
+  for (int j = threadIdx.x; j < K * kStreamClauses; j += blockDim.x)
+    if (j % kStreamClauses >= n_own) s_wt[j] = 0;  // clauses past the own ones (vote tables)
+  if (threadIdx.x < 64) s_vdirty[threadIdx.x] = 0;
   for (int j = threadIdx.x; j < kStreamClauses; j += blockDim.x) {
     s_drop[j] = j < n_own ? a.drop[c_begin + j] == 1u : 1;
     s_pw[j] = j < n_own ? a.patch_w[c_begin + j] : 0;
@@ -2531,6 +2548,8 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
   __syncthreads();
   for (int64_t j = threadIdx.x; j < Wq * kStreamClauses; j += blockDim.x)
     s_maskT[j] = mask_quad((int)(j % kStreamClauses), j / kStreamClauses);
+  if (g.vote_table)
+    for (int e = threadIdx.x; e < 256 * K; e += blockDim.x) s_vt[e] = vt_entry(e);
   // include counts (or emptiness when MAX_INCLUDED_LITERALS >= L), one clause per wave
   for (int idx = wave; idx < n_own; idx += nwv) {
     const uint32_t* m = s_planes + idx * cw + (int64_t)(g.np - 1) * g.W;
@@ -2711,7 +2730,18 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           // (1 .. 1023) into a 16-bit field, so 64 lanes stay below 2^16 and no field carries
           // into the next; the bias of the selected lanes comes off again.
           int kk = 0;
-          if (lds_load(&s_wmax) < 512) {
+          const bool small_w = lds_load(&s_wmax) < 512;
+          if (g.vote_table && small_w) {
+            // lane k < K: its class's vote from the 16 nibbles of the selection mask
+            int acc = 0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int v = (int)((smask >> (4 * j)) & 15ull);
+              acc += lane < K ? (int)s_vt[(j * 16 + v) * K + lane] : 0;
+            }
+            mine = acc;
+            kk = K;
+          } else if (small_w) {
             const int nbias = 512 * __popcll(smask);
             for (; kk + 1 < K; kk += 2) {
               const int v0 = s_wt[kk * kStreamClauses + lane] + 512, v1 = s_wt[(kk + 1) * kStreamClauses + lane] + 512;
@@ -2757,6 +2787,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
     const unsigned long long selm = s_ring[stop & (D - 1)];
     if (threadIdx.x < kStreamClauses) s_selj[threadIdx.x] = ((selm >> threadIdx.x) & 1ull) ? 0 : -1;
     if (threadIdx.x == 0) s_ntask = 0;
+    if (threadIdx.x < 64) s_vdirty[threadIdx.x] = 0;
     for (int j = threadIdx.x; j < K * kStreamClauses; j += blockDim.x) s_wt_old[j] = s_wt[j];
     ++my_stops;
     __syncthreads();
@@ -2780,6 +2811,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           s_w[ix * K + kk] = po.w_new;
           s_wt[kk * kStreamClauses + ix] = (int)po.w_new;
           atomicMax(&s_wmax, (int)po.w_new < 0 ? -(int)po.w_new : (int)po.w_new);
+          if (g.vote_table) atomicOr(&s_vdirty[kk], 1 << (ix >> 2));
         }
         const unsigned long long b1a = __ballot(po.t1a), b1b = __ballot(po.t1b), bt2 = __ballot(po.t2);
         if ((b1a | b1b | bt2) == 0ull) continue;
@@ -2803,6 +2835,15 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       const uint64_t now = __builtin_amdgcn_s_memrealtime();
       prof_acc[2] += now - prof_last;
       prof_last = now;
+    }
+    if (g.vote_table) {
+      // the vote-table entries of the changed weights' nibble groups (read after later
+      // barriers): a wave per class, lanes 0..15 the 16 entries of each changed group
+      for (int k = wave; k < K; k += nwv)
+        for (int dm = s_vdirty[k]; dm; dm &= dm - 1) {
+          const int j = __ffs(dm) - 1;
+          if (lane < 16) s_vt[(j * 16 + lane) * K + k] = vt_entry((j * 16 + lane) * K + k);
+        }
     }
     const int ntask = s_ntask;
     const uint32_t* xe = a.X + (int64_t)stop * g.W;  // the sample's words, for the literal updates

@@ -55,7 +55,8 @@ constexpr int kMaxPlanesHost = 32;  // must equal kMaxPlanes of ytm_device.h
   X(int, group_size)       /* training launch: workgroups per class-sum group */                     \
   X(int, groups)           /* training launch: class-sum groups, ceil(grid / group_size) */          \
   X(int, list_cap)         /* training launch: literal-list capacity per clause (0: none) */       \
-  X(int, mask_lds)         /* training launch, global one-patch kernel: include masks and sample in LDS */
+  X(int, mask_lds)         /* training launch, global one-patch kernel: include masks and sample in LDS */ \
+  X(int, vote_table)       /* training launch, streaming kernel: class votes from nibble tables in LDS */
 
 struct Geom {
 #define YTM_GEOM_DECL(type, name) type name;
