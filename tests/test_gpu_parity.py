@@ -402,6 +402,30 @@ def test_many_classes_injected_and_multioutput(case):
     np.testing.assert_array_equal(mo.score(encX, is_X_encoded=True), refo.score(encX))
 
 
+def test_scoring_lists_follow_the_state():
+    """One-patch scoring keeps its literal lists between calls while the TA states are
+    unchanged: scores after a second call, after more training and after ytm_set_ta_state
+    (load_state_dict) all equal the oracle's."""
+    tm, ref, X, y, Xt, yt = pair(2, 300, 200, clauses=120)
+    encX, encXt = tm.encode(X), tm.encode(Xt)
+    encY = ref.encode_y_multiclass(y)
+    data = tm.device_data(encXt, is_X_encoded=True)
+    tm.fit(encX[:200], y[:200], is_X_encoded=True)
+    ref.fit_encoded(encX[:200], encY[:200])
+    for where in ("first", "again"):
+        np.testing.assert_array_equal(tm.score_device(data), ref.score(encXt), err_msg=where)
+    tm.fit(encX[200:], y[200:], is_X_encoded=True)
+    ref.fit_encoded(encX[200:], encY[200:])
+    np.testing.assert_array_equal(tm.score_device(data), ref.score(encXt), err_msg="after training")
+    rng = np.random.default_rng(8)
+    ta = np.where(rng.random(ref.ta.shape) < 0.02, 200, 60).astype(np.uint32)
+    tm.load_state_dict({"state": {"ta_state": ta, "clause_weights": tm.get_weights(),
+                                  "patch_weights": tm.get_patch_weights(), "min_y": None, "max_y": None}})
+    ref.load_state(ta, ref.w, ref.pw, ref.step)
+    np.testing.assert_array_equal(tm.score_device(data), ref.score(encXt), err_msg="after set_ta_state")
+    data.release()
+
+
 def test_fit_conv_lists_of_literal_indices():
     """Literal lists hold byte offsets into the literal-major sample only while those fit 16
     bits; with 696 literals over 29 patch words ((L-1) * 4 * 29 > 65535) they hold literal

@@ -40,6 +40,11 @@ struct ytm_model {
   size_t sacc_bytes = 0, sout_bytes = 0, slists_bytes = 0;
   void* h_sout = nullptr;  // pinned host staging of the class sums (hipHostMalloc)
   size_t h_sout_bytes = 0;
+  // The TA states change with every fit and ytm_set_ta_state (planes_version counts them);
+  // the one-patch literal lists in d_slists hold those of version slists_version, so that
+  // scoring again an unchanged model does not rebuild them.
+  uint64_t planes_version = 0;
+  uint64_t slists_version = ~0ull;
   // Upper bound of |clause weight|: 1 after initialisation, the largest loaded magnitude
   // after ytm_set_weights, and + 1 per trained sample (a sample moves a weight by at most 1).
   double w_bound = 1.0;
@@ -743,6 +748,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   if (!ds->d_Y) return fail(YTM_EINVAL, "dataset has no targets");
   if (first < 0 || count < 0 || first + count > ds->N) return fail(YTM_EINVAL, "sample range out of bounds");
   if (int rc = check_valid(m)) return rc;
+  ++m->planes_version;  // before any launch: also when the fit fails part-way
   m->stats.last_fit_samples = 0;
   m->stats.last_fit_updates = 0;
   m->stats.last_fit_kernel_ms = 0.0;
@@ -970,13 +976,13 @@ ScorePlan score_plan(const Geom& g, bool has_xt) {
 // (plan.lists_bytes).  Enqueued on the model's stream; the include counts are current when
 // the plan has no lists (the list-based scorers count the literals of their lists).
 hipError_t score_samples(ytm_model* m, const ScorePlan& plan, const uint32_t* X, const uint32_t* XT, int64_t N,
-                         long long* acc, void* lists, float* out) {
+                         long long* acc, void* lists, float* out, bool lists_ready = false) {
   const Geom& g = m->g;
   hipError_t e = hipSuccess;
   if (!plan.chunks) e = ytm::launch_fill_u64((unsigned long long*)acc, N * g.K, m->stream);
   if (e != hipSuccess) return e;
   if (plan.wide)
-    e = ytm::launch_score_wide(m->d_planes, m->d_w, X, N, g, lists, acc, m->stream);
+    e = ytm::launch_score_wide(m->d_planes, m->d_w, X, N, g, lists, lists_ready, acc, m->stream);
   else if (plan.lists_bytes)
     e = ytm::launch_score_lm(m->d_planes, m->d_w, XT, N, g, lists, acc, m->stream);
   else if (plan.chunks)
@@ -1032,7 +1038,11 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   const ScorePlan plan = score_plan(g, ds->d_XT != nullptr);
   hipError_t e = ensure_buffer(&m->d_sacc, &m->sacc_bytes, (size_t)N * plan.acc_per_sample);
   if (e == hipSuccess) e = ensure_buffer(&m->d_sout, &m->sout_bytes, (size_t)(N * g.K) * 4);
+  const void* lists_before = m->d_slists;
   if (e == hipSuccess && plan.lists_bytes) e = ensure_buffer(&m->d_slists, &m->slists_bytes, plan.lists_bytes);
+  if (m->d_slists != lists_before) m->slists_version = ~0ull;
+  // one-patch lists (no literal order) depend on the TA states only: kept from the last call
+  const bool lists_ready = plan.wide && m->slists_version == m->planes_version;
   float* dout = (float*)m->d_sout;
   int rc = YTM_OK;
   // the include counts, for the scorers that read them (the list-based ones count their lists)
@@ -1040,7 +1050,8 @@ int ytm_score_dataset(ytm_model* m, const ytm_dataset* ds, float* class_sums) {
   if (e == hipSuccess) e = hipEventRecord(m->ev0, m->stream);
   if (e == hipSuccess)
     e = score_samples(m, plan, ds->d_X, ds->d_XT, N, (long long*)m->d_sacc, plan.lists_bytes ? m->d_slists : nullptr,
-                      dout);
+                      dout, lists_ready);
+  m->slists_version = e == hipSuccess && plan.wide ? m->planes_version : ~0ull;
   if (e == hipSuccess) e = hipEventRecord(m->ev1, m->stream);
   // the sums come back through a pinned staging buffer of the model (a direct copy into
   // pageable memory goes through the runtime's own staging, in smaller pieces)
@@ -1174,6 +1185,7 @@ int ytm_get_ta_state(ytm_model* m, uint32_t* out) {
 int ytm_set_ta_state(ytm_model* m, const uint32_t* in) {
   if (!m || !in) return fail(YTM_EINVAL, "null argument");
   const Geom& g = m->g;
+  ++m->planes_version;
   // Representable and closed under the feedback dynamics: s' = s + off < 2^np.
   const uint64_t limit = ((uint64_t)1 << g.np) - 1 - g.off;
   for (int64_t i = 0; i < g.C * g.L; ++i)

@@ -44,11 +44,12 @@ hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_
                            void* scratch, long long* acc, hipStream_t s);
 // One patch and clauses wider than 16 words: a tile of samples transposed in LDS, the
 // clauses' literal lists AND-ed lane by lane; scratch holds score_wide_bytes(g); acc (zeroed
-// first) receives each sample's exact sums.
+// first) receives each sample's exact sums.  lists_ready: scratch already holds the lists of
+// these planes (a previous call on the unchanged model), which are then not rebuilt.
 bool score_wide_fits(const Geom& g);
 size_t score_wide_bytes(const Geom& g);  // 0 when score_wide_fits is false
 hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint32_t* X, int64_t N, const Geom& g,
-                             void* scratch, long long* acc, hipStream_t s);
+                             void* scratch, bool lists_ready, long long* acc, hipStream_t s);
 hipError_t launch_score_finish(const long long* acc, const float* bias, int64_t N, const Geom& g,
                                float* out, hipStream_t s);
 // Clause outputs; mode 0: any patch (N, C); 1: per patch (N, C, P); 2: per patch, bit-packed

@@ -1090,10 +1090,12 @@ bool score_wide_fits(const Geom& g) {
 }
 
 hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint32_t* X, int64_t N, const Geom& g,
-                             void* scratch, long long* acc, hipStream_t s) {
+                             void* scratch, bool lists_ready, long long* acc, hipStream_t s) {
   const ListScratch ls = list_scratch(scratch, g);
-  hipError_t err = build_lists(planes, X, nullptr, N, g, ls, s);
-  if (err != hipSuccess) return err;
+  if (!lists_ready) {
+    hipError_t err = build_lists(planes, X, nullptr, N, g, ls, s);
+    if (err != hipSuccess) return err;
+  }
   uint16_t* lists = ls.lists;
   int32_t* nlit = ls.nlit;
   // enough blocks to fill the device (two per CU fit): split the clauses when tiles are few
