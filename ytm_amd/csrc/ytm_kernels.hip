@@ -1233,11 +1233,11 @@ size_t train_lds_bytes(TrainKind kind, int cpw, int rng_slots, const Geom& g) {
   if (kind != TrainKind::kResident)  // task masks [cpw][3] u64; sel, ninc [2][cpw]; task clause / slot [cpw];
                                      // sample [L][PW]; with mask_lds include masks [cpw][W] and samples
                                      // [2][W]; weights [cpw][K]; drop flags [cpw]; with several
-                                     // patches the reservoir thresholds [P+1]
+                                     // patches the reservoir thresholds [P+1] and rank bits [2][cpw]
     return (size_t)3 * cpw * 8 + (size_t)6 * cpw * sizeof(int) + lists +
            (literal_major_lds(g) ? (size_t)(g.L * ((g.P + 31) / 32)) * 4 : 0) +
            (g.mask_lds ? (size_t)(cpw + 2) * g.W * 4 : 0) + (size_t)cpw * g.K * 4 + (size_t)cpw * 4 +
-           (g.P > 1 ? (size_t)(g.P + 1) * 4 : 0);
+           (g.P > 1 ? (size_t)(g.P + 1) * 4 + (size_t)2 * cpw * 4 : 0);
   // Resident kernel (layout of train_resident_body): task masks [cpw][3] u64; planes
   // [cpw][np][W]; weights [cpw][K]; samples [3][W]; sel, ninc [2][cpw]; drop, patch
   // weights [cpw]; targets [3][K]; bias [K]; rank-1 draws [3][cpw]; Q-skip and update

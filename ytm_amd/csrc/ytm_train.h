@@ -111,14 +111,32 @@ __device__ __forceinline__ uint32_t literal_draw_mask(const TrainArgs& a, const 
   }
 }
 
+// The outcomes of ranks 1-4 of a clause's reservoir draws (the first Philox call of its
+// TAG_SEL site): bit r - 1 set when the draw of rank r is below 1.0f / r (r <= P).  Computed
+// by one lane per clause ahead of phase A, so that reservoir_rank needs no Philox call for
+// clauses firing on at most 4 patches.
+__device__ __forceinline__ int rank_bits(const TrainArgs& a, const Geom& g, int64_t c, uint64_t t,
+                                         const float* inv_rank) {
+  const U4 z = counted_site(a, t, (uint32_t)c, TAG_SEL, 0u);
+  int m = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (j + 1 <= g.P && uniform_from_word(word_of(z, j)) < inv_rank[j + 1]) m |= 1 << j;
+  return m;
+}
+
 // Reservoir choice among R >= 1 firing patches (select_active, kernel.cu:285-316): the rank
 // r (1-based, in patch order) of the selected patch is the highest r whose draw is below
 // 1.0f / r, or 0 when none is.  Ranks are scanned from R downward, 256 (64 Philox calls) at
-// a time.  Wave-uniform.
+// a time.  pre >= 0: the clause's rank_bits, which decide R <= 4 alone.  Wave-uniform.
 template <bool INJECT>
 __device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t,
-                                              int R, const float* inv_rank) {
+                                              int R, const float* inv_rank, int pre = -1) {
   const int lane = lane_id();
+  if (!INJECT && pre >= 0 && R <= 4) {
+    const unsigned hits = (unsigned)pre & ((1u << R) - 1u);
+    return hits ? 32 - __builtin_clz(hits) : 0;
+  }
   int best = 0;
   for (int g0 = (R - 1) >> 2; g0 >= 0; g0 -= kWave) {
     const int gl = g0 - lane;
@@ -153,7 +171,7 @@ __device__ __forceinline__ int reservoir_rank(const TrainArgs& a, const Geom& g,
 // Returns -1 when none is selected.  Wave-uniform.
 template <bool INJECT>
 __device__ __forceinline__ int select_from_bitmap(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t,
-                                                  uint32_t acc, const float* inv_rank) {
+                                                  uint32_t acc, const float* inv_rank, int pre = -1) {
   const int lane = lane_id();
   const int PW = (int)((g.P + 31) / 32);
   if (!__any(lane < PW && acc != 0u)) return -1;  // no patch fires (most clauses): no scan
@@ -161,7 +179,7 @@ __device__ __forceinline__ int select_from_bitmap(const TrainArgs& a, const Geom
   const int incl = wave_inclusive_scan(pc);
   const int R = lane_value(incl, kWave - 1);
   if (R == 0) return -1;
-  const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R, inv_rank);
+  const int best = reservoir_rank<INJECT>(a, g, inj, c, t, R, inv_rank, pre);
   if (best == 0) return -1;
   const int excl = incl - pc;
   const bool here = lane < PW && best > excl && best <= incl;
@@ -564,11 +582,11 @@ __device__ int eval_select_lm_group(const TrainArgs& a, const Geom& g, const flo
 // kernel.cu:255-282), taken from the clause's literal list when it has one (nlist <= cap,
 // cap > 0) and from its include mask otherwise.  Then the reservoir choice of the firing
 // patch (select_active, kernel.cu:285-316).  An empty clause fires on every patch in
-// training.  Wave-uniform.
+// training.  pre: the clause's rank_bits for this sample, or -1.  Wave-uniform.
 template <bool INJECT>
 __device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* inj, int64_t c, uint64_t t, const uint32_t* m,
                               const uint16_t* list, int nlist, int cap, const uint32_t* xt, bool dropped,
-                              int* ninc_out, const float* inv_rank) {
+                              int* ninc_out, const float* inv_rank, int pre = -1) {
   const int lane = lane_id();
   int ninc;
   if (cap > 0 && nlist <= cap) {
@@ -589,7 +607,7 @@ __device__ int eval_select_lm(const TrainArgs& a, const Geom& g, const float* in
   uint32_t acc = all_patches_word(g);
   if (ninc != 0)
     acc = (cap > 0 && nlist <= cap) ? firing_from_list(g, list, nlist, xt, acc) : firing_from_mask(g, m, xt, acc);
-  return select_from_bitmap<INJECT>(a, g, inj, c, t, acc, inv_rank);
+  return select_from_bitmap<INJECT>(a, g, inj, c, t, acc, inv_rank, pre);
 }
 
 // Phase A for one clause (wave-uniform): returns the selected patch or -1 and the
@@ -1272,23 +1290,31 @@ __device__ void global_eval_lm_groups(const TrainArgs& a, const Geom& g, const f
   }
 }
 
+// Whether phase A of the global kernel evaluates four clauses to a wave
+// (global_eval_lm_groups): bitmaps of at most 16 words and literal lists.
+template <bool VANILLA>
+__device__ __forceinline__ bool global_grouped(const Geom& g, int cap) {
+  return !VANILLA && literal_major(g) && cap > 0 && (g.P + 31) / 32 <= 16;
+}
+
 // Phase A of sample j over the workgroup's clauses with state in global memory, claimed
 // through *claim: selections and include counts into sel_out / ninc_out, the votes into
 // part.  xt: the literal-major sample (several patches), xe: the sample's words (one
-// patch: with mask_lds its LDS copy), masks: the LDS include masks (mask_lds).
+// patch: with mask_lds its LDS copy), masks: the LDS include masks (mask_lds); s_rb: the
+// own clauses' rank_bits of sample j, or null.
 template <bool VANILLA, bool INJECT>
 __device__ __forceinline__ void global_phase_a(const TrainArgs& a, const Geom& g, int j, int64_t c_begin, int n_own,
                                                int* claim, const uint16_t* s_lits, const int* s_nlit, int cap,
                                                const uint32_t* xt, const uint32_t* xe, const uint32_t* s_mask,
                                                int* sel_out, int* ninc_out, const float* s_wg, long long* part,
-                                               const float* inv_rank, const int* s_drop) {
+                                               const float* inv_rank, const int* s_drop, const int* s_rb) {
   const int lane = lane_id();
   const uint64_t t = a.step0 + (uint64_t)j;
   const float* inj = INJECT ? a.inject + (int64_t)j * a.inject_block : nullptr;
   // Clauses with bitmaps of at most 16 words go four to a wave (eval_select_lm_group).  Two
   // to a wave (32-lane groups) lost on config 4: claims of two clauses balance the waves
   // worse (its phase A + barrier went from 10.8 to 11.5 us per sample).
-  const bool grouped = !VANILLA && literal_major(g) && cap > 0 && (g.P + 31) / 32 <= 16;
+  const bool grouped = global_grouped<VANILLA>(g, cap);
   if (grouped) {
     global_eval_lm_groups<INJECT, 16>(a, g, inj, t, c_begin, n_own, claim, s_lits, s_nlit, xt, sel_out, ninc_out, s_wg,
                                       part, inv_rank, s_drop);
@@ -1304,7 +1330,8 @@ __device__ __forceinline__ void global_phase_a(const TrainArgs& a, const Geom& g
     const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : a.planes + (c * g.np + g.np - 1) * g.W;
     const int sel = (!VANILLA && literal_major(g))
                         ? eval_select_lm<INJECT>(a, g, inj, c, t, m, s_lits + (int64_t)idx * cap,
-                                                 cap > 0 ? s_nlit[idx] : 0, cap, xt, s_drop[idx] != 0, &ninc, inv_rank)
+                                                 cap > 0 ? s_nlit[idx] : 0, cap, xt, s_drop[idx] != 0, &ninc, inv_rank,
+                                                 s_rb ? s_rb[idx] : -1)
                         : eval_select<VANILLA, INJECT>(a, g, inj, c, t, m, xe, s_drop[idx] != 0, -1.0f, &ninc);
     if (lane == 0) {
       sel_out[idx] = sel;
@@ -1366,7 +1393,15 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
   int* s_drop = (int*)(s_wg + (int64_t)cpw * g.K);              // [cpw] dropped (1) or not
   // several patches: the reservoir thresholds 1.0f / r, r = 0..P (a.inv_rank)
   float* s_invr = (float*)(s_drop + cpw);
+  // several patches, counter stream, a clause per wave: the own clauses' rank_bits of
+  // samples j, in buffer j & 1 [2][cpw]
+  int* s_rb = (int*)(s_invr + (g.P > 1 ? g.P + 1 : 0));
   const bool lm = !VANILLA && literal_major(g);
+  const bool use_rb = !INJECT && lm && !global_grouped<VANILLA>(g, cap);
+  auto fill_rb = [&](int j, int first, int count) {
+    for (int idx = first; idx < n_own; idx += count)
+      s_rb[(j & 1) * cpw + idx] = rank_bits(a, g, c_begin + idx, a.step0 + (uint64_t)j, s_invr);
+  };
   unsigned long long my_updates = 0ull, my_fb = 0ull;  // my_fb: samples where some class may update
   uint64_t wait_ticks = 0;
   const uint64_t t_kernel = __builtin_amdgcn_s_memrealtime();
@@ -1392,6 +1427,10 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
                                        s_lits + (int64_t)idx * cap, cap, a.lit_order);
       if (lane == 0) s_nlit[idx] = n;
     }
+  if (use_rb) {  // the rank bits of samples 0 and 1 (from the thresholds, once they are in LDS)
+    __syncthreads();
+    for (int j = 0; j < 2 && j < a.N; ++j) fill_rb(j, threadIdx.x, blockDim.x);
+  }
   // The LDS copy of sample j (threads [first, first + count)): literal-major words, or with
   // mask_lds the words into buffer j & 1.  The sample of phase A / re-evaluation: xt_of,
   // xe_of.
@@ -1477,6 +1516,9 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         if (sl >= 0) atomicAdd(&a.patch_w[(c_begin + idx) * g.P + sl], 1);
       }
       exchange_publish(a, g, i, s_part[b]);
+      // the rank bits of sample i+2 while the sums are in flight (buffer i & 1: sample i's
+      // phase A and re-evaluations are over)
+      if (use_rb && i + 2 < a.N) fill_rb(i + 2, lane, kWave);
       long long S = 0;
       if (exchange_wait(a, g, i, lane < g.K ? lane : 0, lane < g.K, s_part[b], &S, &s_abort, &wait_ticks) &&
           lane < g.K)
@@ -1492,7 +1534,8 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
     // phase A of sample i+1: the other waves from the start, wave 0 once it has the totals
     if (more)
       global_phase_a<VANILLA, INJECT>(a, g, i + 1, c_begin, n_own, &s_next_a, s_lits, s_nlit, cap, xt_of(i + 1),
-                                      xe_of(i + 1), s_mask, sel_n, ninc_n, s_wg, s_part[bn], s_invr, s_drop);
+                                      xe_of(i + 1), s_mask, sel_n, ninc_n, s_wg, s_part[bn], s_invr, s_drop,
+                                      use_rb ? s_rb + ((i + 1) & 1) * cpw : nullptr);
     __syncthreads();
     if (i < 0) {
       prof_last = __builtin_amdgcn_s_memrealtime();
@@ -1619,7 +1662,7 @@ __device__ __forceinline__ void train_global_body(const TrainArgs& a, const Geom
         const uint32_t* m = g.mask_lds ? s_mask + (int64_t)idx * g.W : top;
         const int sel = lm ? eval_select_lm<INJECT>(a, g, injn, c, tn, m, s_lits + (int64_t)idx * cap,
                                                     cap > 0 ? s_nlit[idx] : 0, cap, xt_of(i + 1), s_drop[idx] != 0,
-                                                    &ninc, s_invr)
+                                                    &ninc, s_invr, use_rb ? s_rb[((i + 1) & 1) * cpw + idx] : -1)
                            : eval_select<VANILLA, INJECT>(a, g, injn, c, tn, m, xe_of(i + 1), s_drop[idx] != 0, -1.0f,
                                                           &ninc);
         if (lane == 0) {
