@@ -672,6 +672,30 @@ def test_inference_random_state(dim, patch_dim, classes, clauses):
     assert_packed_equal(tm.transform_patchwise(encX[:9], is_X_encoded=True, packed=True), ref_pw)
 
 
+def test_score_whole_sample_blocks(monkeypatch):
+    """A literal-major copy above 32 KB (1024-thread scoring blocks) and more than 4096
+    clauses: blocks over every clause of a sample (taken from YTM_SCORE_WHOLE_MIN samples
+    on) give the class sums of blocks over chunks of 4096 clauses, and the oracle's."""
+    dim, patch_dim, classes, clauses = (32, 32, 10), (3, 3), 3, 4300
+    kw = dict(number_of_clauses_per_class=clauses, T=50, s=5.0, dim=dim, n_classes=classes, seed=7,
+              patch_dim=patch_dim)
+    tm = MultiClassTM(**kw)
+    ref = orc.OracleTM(clauses, 50, 5.0, dim, classes, patch_dim=patch_dim, seed=7)
+    L, P = tm.number_of_literals, tm.number_of_patches
+    assert L * ((P + 31) // 32) * 4 > 32 * 1024 and tm.number_of_clauses > 4096
+    rng = np.random.default_rng(17)
+    include_p = np.where(rng.random(tm.number_of_clauses) < 0.1, 0.0, 3.0 / L)
+    random_state(tm, ref, rng, include_p)
+    X = (rng.random((20,) + dim) < 0.5).astype(np.uint32).reshape(20, -1)
+    encX = tm.encode(X)
+    monkeypatch.setenv("YTM_SCORE_WHOLE_MIN", "1")
+    whole = tm.score(encX, is_X_encoded=True)
+    monkeypatch.setenv("YTM_SCORE_WHOLE_MIN", "1000000")
+    chunked = tm.score(encX, is_X_encoded=True)
+    np.testing.assert_array_equal(whole, chunked)
+    np.testing.assert_array_equal(whole[:3], ref.score(encX[:3]))
+
+
 @pytest.mark.parametrize("global_state", [False, True])
 def test_fit_random_state_wide_one_patch(monkeypatch, global_state):
     """Training from a random state of a one-patch model with 94-word clauses, some of which

@@ -458,22 +458,34 @@ constexpr int kScoreListCap = 256;
 // (config 3, 13 KB: 256 threads are 19% faster than 1024).
 constexpr int kScoreLmThreads = 1024;
 inline int score_lm_threads(const Geom& g) { return (g.L * ((g.P + 31) / 32)) * 4 > 32 * 1024 ? 1024 : 256; }
+// Clauses per block of score_lm_kernel: kScoreLmChunk, or every clause when the sample's
+// copy is large (1024-thread blocks) and the samples alone give enough blocks to fill the
+// GPU: the copy is then staged once per sample instead of once per 4096 clauses (config 4,
+// 10000 samples: 245K -> 256K samples/s in the kernel).  Small copies keep the chunks (config
+// 3 with one block per sample: 879K -> 855K).  YTM_SCORE_WHOLE_MIN sets the samples needed
+// (default 2048).
+constexpr int64_t kScoreLmWholeMinSamples = 2048;
+inline int64_t score_lm_chunk(const Geom& g, int64_t N) {
+  const char* env = std::getenv("YTM_SCORE_WHOLE_MIN");
+  const int64_t min_n = env && std::atoll(env) > 0 ? std::atoll(env) : kScoreLmWholeMinSamples;
+  return score_lm_threads(g) == 1024 && N >= min_n && g.C > kScoreLmChunk ? g.C : kScoreLmChunk;
+}
 
 template <int FORM>
 __global__ __launch_bounds__(kScoreLmThreads) void score_lm_kernel(const uint32_t* __restrict__ planes,
                                                        const uint16_t* __restrict__ lists,
                                                        const int32_t* __restrict__ nlit, const float* __restrict__ w,
                                                        const uint32_t* __restrict__ XT, int64_t N, Geom g,
-                                                       long long* __restrict__ acc) {
+                                                       int64_t chunk, long long* __restrict__ acc) {
   extern __shared__ uint32_t s_xts[];  // [L][PW]
   const int lane = lane_id();
   // wave-uniform in a scalar register, so that the clause loop and its loads are scalar
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)), nwv = blockDim.x / kWave;
   const int64_t xtw = g.L * ((g.P + 31) / 32);
-  const int64_t nch = (g.C + kScoreLmChunk - 1) / kScoreLmChunk;
+  const int64_t nch = (g.C + chunk - 1) / chunk;
   for (int64_t blk = blockIdx.x; blk < N * nch; blk += gridDim.x) {
     const int64_t e = blk / nch, ch = blk % nch;
-    const int64_t c0 = ch * kScoreLmChunk, c1 = c0 + kScoreLmChunk < g.C ? c0 + kScoreLmChunk : g.C;
+    const int64_t c0 = ch * chunk, c1 = c0 + chunk < g.C ? c0 + chunk : g.C;
     __syncthreads();  // the previous sample is no longer read
     copy_to_lds(s_xts, XT + e * xtw, xtw, threadIdx.x, blockDim.x);
     __syncthreads();
@@ -1072,14 +1084,15 @@ hipError_t launch_score_lm(const uint32_t* planes, const float* w, const uint32_
   if (err != hipSuccess) return err;
   uint16_t* lists = ls.lists;
   int32_t* nlit = ls.nlit;
-  const int64_t blocks = N * ((g.C + kScoreLmChunk - 1) / kScoreLmChunk);
+  const int64_t chunk = score_lm_chunk(g, N);
+  const int64_t blocks = N * ((g.C + chunk - 1) / chunk);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
   const size_t lds = (size_t)(g.L * ((g.P + 31) / 32)) * 4;
   // the sample fits LDS (score_lists_bytes), so its word offsets fit 16 bits: no kListIndex
   if (list_form(g) == kListBytes)
-    score_lm_kernel<kListBytes><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, w, XT, N, g, acc);
+    score_lm_kernel<kListBytes><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, w, XT, N, g, chunk, acc);
   else
-    score_lm_kernel<kListWords><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, w, XT, N, g, acc);
+    score_lm_kernel<kListWords><<<grid, score_lm_threads(g), lds, s>>>(planes, lists, nlit, w, XT, N, g, chunk, acc);
   return hipGetLastError();
 }
 
