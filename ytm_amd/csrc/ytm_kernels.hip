@@ -424,10 +424,7 @@ __device__ __forceinline__ uint32_t firing_from_list_regs(const Geom& g, uint4 l
         const unsigned long long live = __ballot(part != 0u);
         dead = __any(in_group && ((live >> (q * GS)) & gmask) == 0ull);
       }
-      if (dead) {
-        part = 0u;
-        break;
-      }
+      if (dead) return 0u;  // nothing fires: no combination of the groups
     }
     uint32_t r = part;
     for (int gq = 1; gq < NG; ++gq)
@@ -471,12 +468,16 @@ inline int64_t score_lm_chunk(const Geom& g, int64_t N) {
   return score_lm_threads(g) == 1024 && N >= min_n && g.C > kScoreLmChunk ? g.C : kScoreLmChunk;
 }
 
+// Eight waves per SIMD (the compiler keeps at most 64 VGPRs and moves SGPRs it cannot keep
+// to VGPR lanes): at the default seven, SGPR-bound, a CU held one 1024-thread block of a
+// 64 KB copy; now two (config 4 inference 269K -> 327K samples/s in the kernel, config 3
+// 930K -> 999K).  The one-patch tile and wide scorers lost with the same bound (config 1
+// 430M -> 356M, config 2 160M -> 157M) and keep the default.
 template <int FORM>
-__global__ __launch_bounds__(kScoreLmThreads) void score_lm_kernel(const uint32_t* __restrict__ planes,
-                                                       const uint16_t* __restrict__ lists,
-                                                       const int32_t* __restrict__ nlit, const float* __restrict__ w,
-                                                       const uint32_t* __restrict__ XT, int64_t N, Geom g,
-                                                       int64_t chunk, long long* __restrict__ acc) {
+__global__ __launch_bounds__(kScoreLmThreads) __attribute__((amdgpu_waves_per_eu(8))) void score_lm_kernel(
+    const uint32_t* __restrict__ planes, const uint16_t* __restrict__ lists, const int32_t* __restrict__ nlit,
+    const float* __restrict__ w, const uint32_t* __restrict__ XT, int64_t N, Geom g, int64_t chunk,
+    long long* __restrict__ acc) {
   extern __shared__ uint32_t s_xts[];  // [L][PW]
   const int lane = lane_id();
   // wave-uniform in a scalar register, so that the clause loop and its loads are scalar
