@@ -1118,8 +1118,14 @@ hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint3
   const int64_t nch = want < most ? want : most;
   const int64_t blocks = tiles * (nch > 0 ? nch : 1);
   const int grid = blocks < 65536 ? (int)blocks : 65536;
-  wide_kernel<false><<<grid, 1024, (size_t)(g.W * 32) * 4, s>>>(planes, lists, nlit, w, X, N, g, nch > 0 ? nch : 1,
-                                                                 acc, nullptr);
+  // 512 threads when two such blocks fit a CU's LDS: at 92 VGPRs a CU holds 20 waves, so one
+  // 1024-thread block or two of 512, whose transposes, barriers and walks then overlap
+  // (config 2, 6 KB per block: 159M -> 178M samples/s in the kernel); a transposed tile
+  // above 64 KB keeps 1024 (config 5, 80 KB: one 512-thread block per CU would halve the
+  // waves, 2.0M -> 1.05M).
+  const size_t lds = (size_t)(g.W * 32) * 4;
+  const int threads = lds <= 64 * 1024 ? 512 : 1024;
+  wide_kernel<false><<<grid, threads, lds, s>>>(planes, lists, nlit, w, X, N, g, nch > 0 ? nch : 1, acc, nullptr);
   return hipGetLastError();
 }
 
