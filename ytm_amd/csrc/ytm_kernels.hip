@@ -660,12 +660,12 @@ __global__ __launch_bounds__(256) void tile_kernel(const uint32_t* __restrict__ 
 // firing bitmap over all patches is the AND of the included literals' bitsets (from the
 // clause's literal list when it has one).  MODE 0: out[e][c] = some patch fires;
 // MODE 1: out[e][c][p]; MODE 2: out[e][c][j] with bit b = patch 32j + b (0 beyond P).
+// Eight waves per SIMD, as score_lm_kernel (configs 3 and 4, 1000 samples, six calls: 18.0 ->
+// 13.0 ms in the kernel).
 template <int MODE, int FORM>
-__global__ __launch_bounds__(kScoreLmThreads) void transform_lm_kernel(const uint32_t* __restrict__ planes,
-                                                           const uint16_t* __restrict__ lists,
-                                                           const int32_t* __restrict__ nlit,
-                                                           const uint32_t* __restrict__ XT, int64_t N, Geom g,
-                                                           uint32_t* __restrict__ out) {
+__global__ __launch_bounds__(kScoreLmThreads) __attribute__((amdgpu_waves_per_eu(8))) void transform_lm_kernel(
+    const uint32_t* __restrict__ planes, const uint16_t* __restrict__ lists, const int32_t* __restrict__ nlit,
+    const uint32_t* __restrict__ XT, int64_t N, Geom g, uint32_t* __restrict__ out) {
   extern __shared__ uint32_t s_xts[];  // [L][PW]
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)), nwv = blockDim.x / kWave;
