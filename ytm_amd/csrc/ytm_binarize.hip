@@ -70,6 +70,12 @@ struct BinnedPixels {
     const int j = (int)(f - i * width);
     return bin_level<C, ONEHOT>(as_cmp<T, C>(X[e * Fr + i]), t, nthr, edge, width, j);
   }
+  // the same for f < 2^31, in 32-bit arithmetic (encode_staged)
+  __device__ __forceinline__ bool bit32(int64_t e, int f) const {
+    const int i = (int)((unsigned)f / (unsigned)width);
+    const int j = f - i * width;
+    return bin_level<C, ONEHOT>(as_cmp<T, C>(X[e * Fr + i]), t, nthr, edge, width, j);
+  }
 };
 
 // encode of the binned raw values of N samples (encode_words, ytm_encode.h): the same words
@@ -80,6 +86,15 @@ __global__ __launch_bounds__(256) void encode_binned_kernel(const T* __restrict_
                                                             uint32_t* __restrict__ out, Geom g) {
   const int width = ONEHOT ? nthr - 1 + (edge ? 2 : 0) : nthr;
   encode_words(BinnedPixels<T, C, ONEHOT>{X, Fr, t, nthr, edge, width}, N, out, g);
+}
+
+// Several patches: a block per sample, its binned pixel bits staged in LDS (encode_staged).
+template <typename T, typename C, bool ONEHOT>
+__global__ __launch_bounds__(256) void encode_binned_staged_kernel(const T* __restrict__ X, int64_t N, int64_t Fr,
+                                                                   const C* __restrict__ t, int nthr, int edge,
+                                                                   uint32_t* __restrict__ out, Geom g) {
+  const int width = ONEHOT ? nthr - 1 + (edge ? 2 : 0) : nthr;
+  encode_staged(BinnedPixels<T, C, ONEHOT>{X, Fr, t, nthr, edge, width}, N, out, g);
 }
 
 // Collapse of binned rows (binarizer.py:88-105): thermometer -> index of the last non-zero
@@ -143,10 +158,15 @@ hipError_t launch_typed(const void* X, int dtype, int64_t n, const C* t, int nth
 template <typename C, bool ONEHOT>
 hipError_t launch_encode_typed(const void* X, int dtype, int64_t N, int64_t Fr, const C* t, int nthr, int edge,
                                uint32_t* out, const Geom& g, hipStream_t s) {
-  const int grid = grid_of(N * g.P * g.W);
-#define YTM_ENC_CASE(code, T)                                                                          \
-  case code:                                                                                           \
-    encode_binned_kernel<T, C, ONEHOT><<<grid, 256, 0, s>>>((const T*)X, N, Fr, t, nthr, edge, out, g); \
+  const bool staged = encode_staged_fits(g);
+  const int grid = staged ? (int)(N < 65536 ? (N > 0 ? N : 1) : 65536) : grid_of(N * g.P * g.W);
+  const size_t lds = staged ? (size_t)encode_staged_lds_bytes(g) : 0;
+#define YTM_ENC_CASE(code, T)                                                                                    \
+  case code:                                                                                                     \
+    if (staged)                                                                                                  \
+      encode_binned_staged_kernel<T, C, ONEHOT><<<grid, 256, lds, s>>>((const T*)X, N, Fr, t, nthr, edge, out, g); \
+    else                                                                                                         \
+      encode_binned_kernel<T, C, ONEHOT><<<grid, 256, 0, s>>>((const T*)X, N, Fr, t, nthr, edge, out, g);         \
     break;
   switch (dtype) {
     YTM_ENC_CASE(YTM_DTYPE_U8, uint8_t)

@@ -14,6 +14,7 @@ struct PlainPixels {
   const uint32_t* X;
   int64_t F;  // values per sample
   __device__ __forceinline__ bool operator()(int64_t e, int64_t f) const { return X[e * F + f] > 0u; }
+  __device__ __forceinline__ bool bit32(int64_t e, int f) const { return X[e * F + f] > 0u; }
 };
 
 // Positive literal li of patch (py, px) of sample e, the pixels read through pix(e, f) with
@@ -66,6 +67,97 @@ __device__ __forceinline__ void encode_words(const Pix& pix, int64_t N, uint32_t
       word |= bit << b;
     }
     out[idx] = word;
+  }
+}
+
+// Several patches: the same words as encode_words, a block per sample at a time.  The
+// sample's F pixel bits pix(e, f) are staged in LDS as a bitmap first (each wave ballots 64
+// consecutive bits; one evaluation of pix per bit instead of one per output bit: config 4
+// reads each binned pixel bit in up to 9 patches).  Then each thread builds whole words:
+// the pixel literals of one patch row are consecutive pixel values (f = patch origin +
+// ry * image row + rx * dim2 + z, with rx * dim2 + z running over pd0 * dim2 values), so a
+// word takes its pixel literals as a few bit ranges of the bitmap instead of bit by bit.  A
+// word holds at most two runs of positive-literal indices: its positive literals, then
+// (with appended negations) the negated ones.
+constexpr int64_t kEncodeStagedMaxBits = 256 * 1024;  // a 32 KB LDS bitmap
+
+__host__ __device__ constexpr bool encode_staged_fits(const Geom& g) {
+  return g.P > 1 && g.F <= kEncodeStagedMaxBits && g.P * g.W < (int64_t(1) << 31);
+}
+
+__host__ __device__ constexpr int64_t encode_staged_lds_bytes(const Geom& g) { return (g.F + 31) / 32 * 4; }
+
+// Bits [lo, hi) of a 32-bit word (clamped to [0, 32)).
+__device__ __forceinline__ uint32_t bit_range(int lo, int hi) {
+  lo = lo < 0 ? 0 : lo;
+  hi = hi > 32 ? 32 : hi;
+  if (hi <= lo) return 0u;
+  const uint32_t upto = hi == 32 ? 0xFFFFFFFFu : ((1u << hi) - 1u);
+  return upto & ~((1u << lo) - 1u);
+}
+
+template <typename Pix>
+__device__ __forceinline__ void encode_staged(const Pix& pix, int64_t N, uint32_t* __restrict__ out, const Geom& g) {
+  extern __shared__ uint32_t s_bits[];  // [ceil(F / 32)]
+  const int F = (int)g.F, FW = (F + 31) / 32;
+  const int W = (int)g.W, PWw = (int)(g.P * g.W);
+  const int xw = g.dim0 - g.pd0 + 1;
+  const int ty = g.dim1 - g.pd1, tx = g.dim0 - g.pd0;
+  const int row = g.pd0 * g.dim2;        // pixel literals per patch row
+  const int img_row = g.dim0 * g.dim2;   // pixel values per image row
+  const bool loc_on = g.encode_loc != 0;
+  const int loc = loc_on ? ty + tx : 0;  // literals before the patch pixels
+  const int L = (int)g.L, Lh = (int)g.Lh;
+  const bool an = g.append_negated != 0;
+  const int lane = (int)(threadIdx.x & (kWave - 1)), wv = (int)(threadIdx.x / kWave);
+  const int nwv = (int)(blockDim.x / kWave);
+  for (int64_t e = blockIdx.x; e < N; e += gridDim.x) {
+    __syncthreads();  // the previous sample's bits are no longer read
+    for (int f0 = wv * kWave; f0 < F; f0 += nwv * kWave) {
+      const int f = f0 + lane;
+      const unsigned long long m = __ballot(f < F && pix.bit32(e, f));
+      if (lane == 0) s_bits[f0 >> 5] = (uint32_t)m;
+      if (lane == 1 && (f0 >> 5) + 1 < FW) s_bits[(f0 >> 5) + 1] = (uint32_t)(m >> 32);
+    }
+    __syncthreads();
+    uint32_t* oe = out + e * (int64_t)PWw;
+    for (int idx = threadIdx.x; idx < PWw; idx += blockDim.x) {
+      const int p = idx / W, w = idx - p * W;
+      const int py = p / xw, px = p - py * xw;
+      const int base = py * img_row + px * g.dim2;  // pixel value of the patch origin
+      const int l0 = w * 32, l1 = l0 + 32 < L ? l0 + 32 : L;
+      uint32_t word = 0u;
+      for (int seg = 0; seg < 2; ++seg) {
+        const bool neg = seg == 1;
+        if (neg && !an) break;
+        int l = neg ? (l0 > Lh ? l0 : Lh) : l0;
+        const int bnd = (an && !neg) ? (l1 < Lh ? l1 : Lh) : l1;
+        int li = neg ? l - Lh : l;  // positive literal index
+        for (; l < bnd && li < loc; ++l, ++li) {  // the position thermometers (encode_loc)
+          const uint32_t bit = li < ty ? (li < py ? 1u : 0u) : ((li - ty) < px ? 1u : 0u);
+          word |= (bit ^ (neg ? 1u : 0u)) << (l - l0);
+        }
+        while (l < bnd) {  // pixel literals, up to the end of a patch row at a time
+          const int pi = li - loc;
+          const int ry = pi / row, c = pi - ry * row;
+          const int k = row - c < bnd - l ? row - c : bnd - l;  // 1..32
+          const int f = base + ry * img_row + c;
+          const int w0 = f >> 5;
+          const unsigned long long two =
+              (unsigned long long)s_bits[w0] | ((unsigned long long)s_bits[w0 + 1 < FW ? w0 + 1 : w0] << 32);
+          const uint32_t keep = k == 32 ? 0xFFFFFFFFu : ((1u << k) - 1u);
+          uint32_t bits = (uint32_t)(two >> (f & 31)) & keep;
+          // without encode_loc the thermometers still overwrite the first pixel literals
+          // (positive_literal): literal li + t with li + t < py or ty <= li + t < ty + px
+          if (!loc_on) bits |= (bit_range(0, py - li) | bit_range(ty - li, ty + px - li)) & keep;
+          if (neg) bits = ~bits & keep;
+          word |= bits << (l - l0);
+          l += k;
+          li += k;
+        }
+      }
+      oe[idx] = word;
+    }
   }
 }
 

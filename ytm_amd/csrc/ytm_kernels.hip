@@ -23,6 +23,12 @@ __global__ __launch_bounds__(256) void encode_kernel(const uint32_t* __restrict_
   encode_words(PlainPixels{X, g.F}, N, out, g);
 }
 
+// Several patches: a block per sample, its pixel bits staged in LDS (encode_staged).
+__global__ __launch_bounds__(256) void encode_staged_kernel(const uint32_t* __restrict__ X, int64_t N,
+                                                            uint32_t* __restrict__ out, Geom g) {
+  encode_staged(PlainPixels{X, g.F}, N, out, g);
+}
+
 // Literal-major copy of encoded samples with several patches: bit b of XT[e][l][j] is
 // literal l of patch 32j + b (0 beyond P), PW = ceil(P / 32) words per literal.  One wave
 // per (sample, literal word w, chunk of 64 patches): lane q holds word w of patch
@@ -874,7 +880,12 @@ static int grid_for(int64_t items, int block) {
 }
 
 hipError_t launch_encode(const uint32_t* X, int64_t N, uint32_t* out, const Geom& g, hipStream_t s) {
-  encode_kernel<<<grid_for(N * g.P * g.W, 256), 256, 0, s>>>(X, N, out, g);
+  if (encode_staged_fits(g)) {
+    if (N > 0)
+      encode_staged_kernel<<<(int)(N < 65536 ? N : 65536), 256, encode_staged_lds_bytes(g), s>>>(X, N, out, g);
+  } else {
+    encode_kernel<<<grid_for(N * g.P * g.W, 256), 256, 0, s>>>(X, N, out, g);
+  }
   return hipGetLastError();
 }
 
