@@ -56,13 +56,14 @@ def test_encode(cfg, n):
 
 
 @pytest.mark.parametrize("dim,patch_dim", [((7, 6, 2), (3, 2)), ((12, 12, 3), (4, 5)), ((5, 9, 1), (5, 2)),
-                                           ((33, 4, 1), (33, 2))])
+                                           ((33, 4, 1), (33, 2)), ((5000, 1, 1), (5000, 1)), ((70, 70, 1), (70, 70))])
 @pytest.mark.parametrize("encode_loc,append_negated", [(True, True), (False, True), (True, False), (False, False)])
 def test_encode_several_patch_variants(dim, patch_dim, encode_loc, append_negated):
     """The several-patch encoder (a block per sample, its pixel bits staged in LDS, a word's
     pixel literals taken as bit ranges of patch rows) against the oracle with and without
     position thermometers and appended negations, on patch shapes whose words hold ranges
-    across rows, patches and the negated half, and a patch row longer than a word."""
+    across rows, patches and the negated half, and a patch row longer than a word; also one
+    patch of 313 and 307 words, which takes the same encoder."""
     kw = dict(patch_dim=patch_dim, encode_loc=encode_loc, append_negated=append_negated, seed=3)
     tm = MultiClassTM(10, 15, 3.9, dim=dim, n_classes=2, **kw)
     ref = orc.OracleTM(10, 15, 3.9, dim, 2, **kw)

@@ -70,10 +70,11 @@ __device__ __forceinline__ void encode_words(const Pix& pix, int64_t N, uint32_t
   }
 }
 
-// Several patches: the same words as encode_words, a block per sample at a time.  The
-// sample's F pixel bits pix(e, f) are staged in LDS as a bitmap first (each wave ballots 64
-// consecutive bits; one evaluation of pix per bit instead of one per output bit: config 4
-// reads each binned pixel bit in up to 9 patches).  Then each thread builds whole words:
+// Several patches (or one wide patch): the same words as encode_words, a block per sample
+// at a time.  The sample's F pixel bits pix(e, f) are staged in LDS as a bitmap first (each
+// wave ballots 64 consecutive bits; one evaluation of pix per bit instead of one per output
+// bit: config 4 reads each binned pixel bit in up to 9 patches).  Then each thread builds
+// whole words:
 // the pixel literals of one patch row are consecutive pixel values (f = patch origin +
 // ry * image row + rx * dim2 + z, with rx * dim2 + z running over pd0 * dim2 values), so a
 // word takes its pixel literals as a few bit ranges of the bitmap instead of bit by bit.  A
@@ -81,8 +82,9 @@ __device__ __forceinline__ void encode_words(const Pix& pix, int64_t N, uint32_t
 // (with appended negations) the negated ones.
 constexpr int64_t kEncodeStagedMaxBits = 256 * 1024;  // a 32 KB LDS bitmap
 
+// Several patches, or one patch of enough words to occupy a block (config 5: 625).
 __host__ __device__ constexpr bool encode_staged_fits(const Geom& g) {
-  return g.P > 1 && g.F <= kEncodeStagedMaxBits && g.P * g.W < (int64_t(1) << 31);
+  return (g.P > 1 || g.W >= 128) && g.F <= kEncodeStagedMaxBits && g.P * g.W < (int64_t(1) << 31);
 }
 
 __host__ __device__ constexpr int64_t encode_staged_lds_bytes(const Geom& g) { return (g.F + 31) / 32 * 4; }
