@@ -896,11 +896,14 @@ __device__ __forceinline__ int tasks_per_wave(const Geom& g, int ntask, int nwv)
 // relative to the clause's first class), first draw slot s_task_sb[tk] (s_rng null: draws
 // computed here); sel_of[idx] the clause's selected patch; planes of clause idx at
 // planes_base + idx * np * W; xe the sample's patch-major words.
+// changed_lanes, when given, receives the ballot of the lanes whose include-mask word (top
+// plane) changed: task tk0 + g changed its mask when a bit of [g * W, g * W + W) is set.
 template <bool INJECT>
 __device__ void apply_tasks(const TrainArgs& a, const Geom& g, const float* inj, int64_t c_begin, uint64_t t, int tk0,
                             int per, int ntask, const int* s_task_idx, const unsigned long long* s_task_m,
                             const int* s_task_sb, const int* sel_of, uint32_t* planes_base, const uint32_t* xe,
-                            const uint32_t* s_rng, int R, uint32_t* top_base = nullptr) {
+                            const uint32_t* s_rng, int R, uint32_t* top_base = nullptr,
+                            unsigned long long* changed_lanes = nullptr) {
   const int lane = lane_id();
   const int W = (int)g.W;
   const int grp = lane / W, w = lane % W;
@@ -947,6 +950,7 @@ __device__ void apply_tasks(const TrainArgs& a, const Geom& g, const float* inj,
     // Type II (kernel.cu:481-506): literal 0 -> +1, no upper guard.
     if (__any(is2)) planes_inc(pl, np, is2 ? (~xb & F) : 0u);
   }
+  if (changed_lanes) *changed_lanes = __ballot(act && pw[(int64_t)(np - 1) * W] != pl[np - 1]);
   if (act) {
 #pragma unroll
     for (int j = 0; j < kMaxPlanes; ++j)
@@ -1978,6 +1982,21 @@ __device__ __forceinline__ void commit_fused_task(const TrainArgs& a, const Geom
   if (lane == 0 && spec_sel >= 0 && g.P == 1) s_pw[idx] -= 1;
 }
 
+// The votes of resident clause idx for the sample after the feedback again, with its new
+// weights, when its literal updates left the include mask as it was: its evaluation (the
+// selection sel and the include count) on that sample stands, so only what resident_eval
+// adds after the evaluation is redone.
+__device__ __forceinline__ void resident_revote(const Geom& g, int64_t c_begin, int idx, int sel, const float* s_w,
+                                                int* s_pw, long long* part) {
+  const int lane = lane_id();
+  if (sel < 0) return;
+  const int64_t c = c_begin + idx;
+  const int64_t kp = g.coalesced ? (lane < g.K ? lane : 0) : c / g.per_bank;
+  if (lane == 0 && g.P == 1) s_pw[idx] += 1;
+  if (g.coalesced ? lane < g.K : lane == 0)
+    atomicAdd((unsigned long long*)&part[kp], (unsigned long long)(long long)s_w[idx * g.K + kp]);
+}
+
 // Training with each workgroup's clause state resident in LDS for the whole launch:
 // planes [own][np][W], weights [own][K] (and, with one patch, patch weights [own]) are
 // loaded once, updated in place and written back at the end.  With several patches the
@@ -2405,19 +2424,29 @@ __device__ __forceinline__ void train_resident_body(const TrainArgs& a, const Ge
             commit_fused_task(a, g, c_begin, idx, more ? s_sel[b2n * cpw + idx] : -1, s_task_w + tk * g.K, s_w,
                               s_part[b2n], s_pw);
           }
+        unsigned long long chg = 0ull;
         apply_tasks<INJECT>(a, g, inj, c_begin, t, tk0, per, ntask, s_task_idx, s_task_m, s_task_sb,
-                            s_sel + b2 * cpw, s_planes, xe, INJECT ? nullptr : s_rng, R);
+                            s_sel + b2 * cpw, s_planes, xe, INJECT ? nullptr : s_rng, R, nullptr, &chg);
+        const unsigned long long wmask = (1ull << g.W) - 1ull;
+        // a task whose include mask is unchanged keeps its list and its evaluation of sample
+        // i+1; only its votes come back with the new weights (resident_revote)
         if (cap > 0)
           for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk) {
+            if (((chg >> ((tk - tk0) * g.W)) & wmask) == 0ull) continue;
             const int idx = s_task_idx[tk];
             const int n = build_literal_list(g, s_planes + idx * cw + (int64_t)(g.np - 1) * g.W,
                                              s_lits + (int64_t)idx * cap, cap, a.lit_order);
             if (lane == 0) s_nlit[idx] = n;
           }
         if (more)
-          for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk)
-            resident_eval<INJECT>(a, g, i + 1, c_begin, s_task_idx[tk], s_planes, s_w, s_drop, s_x, s_xt, s_usel,
-                                  s_invr, s_lits, s_nlit, s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+          for (int tk = tk0; tk < tk0 + per && tk < ntask; ++tk) {
+            const int idx = s_task_idx[tk];
+            if (((chg >> ((tk - tk0) * g.W)) & wmask) == 0ull)
+              resident_revote(g, c_begin, idx, s_sel[b2n * cpw + idx], s_w, s_pw, s_part[b2n]);
+            else
+              resident_eval<INJECT>(a, g, i + 1, c_begin, idx, s_planes, s_w, s_drop, s_x, s_xt, s_usel, s_invr,
+                                    s_lits, s_nlit, s_sel + b2n * cpw, s_ninc + b2n * cpw, s_pw, s_part[b2n]);
+          }
       }
     } else {
       for (int tk = wave; tk < ntask; tk += nwv) {  // tasks round-robin over the waves
