@@ -155,9 +155,10 @@ def test_fit_resident_kernel_counter_stream(monkeypatch, cfg, n, clauses, epochs
 
 
 def test_stream_kernel_choice_follows_feedback():
-    """One-patch models train on the streaming kernel unless the last fit had feedback at half
-    of its samples or more (then the resident kernel); the counts of samples with feedback
-    agree between the kernels, and every fit matches the oracle."""
+    """A new model updates at nearly every sample, so one-patch models start on the resident
+    kernel and stay there while the feedback share is at half of the samples or more (config
+    1, noisy XOR: every epoch); the counts of samples with feedback agree between the
+    kernels, and every fit matches the oracle."""
     tm, ref, X, y, *_ = pair(1, 3000)
     encX = tm.encode(X)
     encY = ref.encode_y_multiclass(y)
@@ -170,7 +171,31 @@ def test_stream_kernel_choice_follows_feedback():
         assert st["last_fit_updates"] == upd
         assert_state_equal(tm, ref, f"epoch {epoch}")
         assert st["last_fit_feedback_samples"] > 1500  # noisy XOR: feedback at nearly every sample
-    assert kinds == [3, 0, 0]
+    assert kinds == [0, 0, 0]
+
+
+def test_first_epoch_in_segments():
+    """The first fits of a new config-2 model go in segments of 4096 samples on the resident
+    kernel while the feedback share stays at half or more, then on the streaming kernel for
+    the rest (config 2 on 12000 samples: feedback at 82% of the first epoch's samples, 45%
+    of the second's); once the share is low a fit streams in one launch.  Update and
+    feedback counts add up over the segments, and every fit matches the oracle."""
+    tm, ref, X, y, *_ = pair(2, 12000)
+    encX = tm.encode(X)
+    encY = ref.encode_y_multiclass(y)
+    for epoch in range(4):
+        upd = ref.fit_encoded(encX, encY)
+        tm.fit(encX, y, is_X_encoded=True)
+        st = tm.stats()
+        print(f"[segments] epoch {epoch}: kind {st['train_kind']} launches {st['last_fit_launches']} "
+              f"feedback samples {st['last_fit_feedback_samples']} updates {upd}", flush=True)
+        assert st["last_fit_updates"] == upd, f"update count epoch {epoch}"
+        assert st["last_fit_feedback_samples"] == ref.last_feedback_samples
+        assert st["last_fit_samples"] == 12000
+        assert_state_equal(tm, ref, f"epoch {epoch}")
+        if epoch == 0:
+            assert st["last_fit_launches"] >= 2
+    assert st["train_kind"] == 3 and st["last_fit_launches"] == 1
 
 
 @pytest.mark.parametrize("wgs,threads,gens", [("", "", ""), ("7", "", ""), ("31", "512", ""), ("64", "256", ""),

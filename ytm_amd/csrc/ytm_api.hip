@@ -52,7 +52,9 @@ struct ytm_model {
   // the state is then a mix of samples: the model refuses fit, score and transform until a
   // whole state is loaded again (the bits of the setters called since: 1 TA states, 2
   // weights, 4 patch weights).
-  double feedback_frac = 0.0;  // share of the last fit's samples where some class could update
+  // share of the last fit's samples where some class could update; a new model updates at
+  // nearly every sample (its class sums start near 0, with update probability about 1/2)
+  double feedback_frac = 1.0;
   bool invalid = false;
   int reloaded = 0;
   ytm_stats stats;
@@ -742,12 +744,71 @@ void ytm_dataset_destroy(ytm_dataset* ds) {
   delete ds;
 }
 
+namespace {
+// Feedback share below which one-patch models stream: per sample the streaming kernel costs
+// about 0.2 us plus 6-7 us per sample with feedback, the resident kernel about 3 us (config 2,
+// epoch 1 in segments of 10000 samples: at 85% feedback streaming took 75 ms, at 53% 38 ms,
+// at 35% 25 ms; resident 28-35 ms; config 1 at 96%: resident 11% faster).
+constexpr double kStreamBelow = 0.55;
+int fit_range(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count, const uint32_t* drop,
+              const float* inject);
+}
+
+// Samples [first, first + count) in order.  A fit of at least 8192 samples of a one-patch
+// model that the streaming kernel can take goes in segments while its recent feedback share
+// is at kStreamBelow or more (the resident kernel then, re-decided after each segment of a
+// sixth of the fit, at least 4096 samples), the rest in one streaming launch: the first
+// epoch of a new model starts with feedback at nearly every sample and ends with few (config
+// 2: 85% of the first 10000 samples, 53% of the next, 19% of the last).  The statistics add
+// up over the segments.
 int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count, const uint32_t* drop,
                     const float* inject) {
   if (!m || !ds || ds->m != m) return fail(YTM_EINVAL, "dataset does not belong to this model");
   if (!ds->d_Y) return fail(YTM_EINVAL, "dataset has no targets");
   if (first < 0 || count < 0 || first + count > ds->N) return fail(YTM_EINVAL, "sample range out of bounds");
   if (int rc = check_valid(m)) return rc;
+  const char* stream_env = std::getenv("YTM_TRAIN_STREAM");
+  const char* force_global = std::getenv("YTM_TRAIN_GLOBAL");
+  Geom gs;
+  const bool segmented = !stream_env && !(force_global && std::atoi(force_global) > 0) && count >= 8192 &&
+                         !per_sample_training(m->g) && stream_geometry(m, inject != nullptr, false, count, &gs);
+  if (!segmented) return fit_range(m, ds, first, count, drop, inject);
+  const int64_t seg = std::max<int64_t>(4096, count / 6);
+  const int64_t block = m->g.C * m->g.P + 2 * m->g.C * m->g.K + m->g.C * m->g.K * m->g.L;  // injected floats per sample
+  ytm_stats sum = m->stats;
+  sum.last_fit_samples = sum.last_fit_updates = sum.last_fit_feedback_samples = sum.last_fit_evaluations = 0;
+  sum.last_fit_kernel_ms = 0.0;
+  sum.last_fit_launches = 0;
+  double phase[8] = {0, 0, 0, 0, 0, 0, 0, 0}, wait_ms = 0.0;
+  for (int64_t s = 0; s < count;) {
+    const int64_t n = m->feedback_frac < kStreamBelow ? count - s : std::min(seg, count - s);
+    if (int rc = fit_range(m, ds, first + s, n, drop, inject ? inject + s * block : nullptr)) return rc;
+    const ytm_stats& st = m->stats;
+    sum.last_fit_samples += st.last_fit_samples;
+    sum.last_fit_updates += st.last_fit_updates;
+    sum.last_fit_feedback_samples += st.last_fit_feedback_samples;
+    sum.last_fit_evaluations += st.last_fit_evaluations;
+    sum.last_fit_kernel_ms += st.last_fit_kernel_ms;
+    sum.last_fit_launches += st.last_fit_launches;
+    for (int j = 0; j < 8; ++j) phase[j] += st.last_fit_phase_us[j] * (double)n;
+    wait_ms += st.last_fit_wait_frac * st.last_fit_kernel_ms;
+    s += n;
+  }
+  ytm_stats& st = m->stats;  // step, total updates and the last segment's kernel stay as they are
+  st.last_fit_samples = sum.last_fit_samples;
+  st.last_fit_updates = sum.last_fit_updates;
+  st.last_fit_feedback_samples = sum.last_fit_feedback_samples;
+  st.last_fit_evaluations = sum.last_fit_evaluations;
+  st.last_fit_kernel_ms = sum.last_fit_kernel_ms;
+  st.last_fit_launches = sum.last_fit_launches;
+  for (int j = 0; j < 8; ++j) st.last_fit_phase_us[j] = phase[j] / (double)count;
+  st.last_fit_wait_frac = sum.last_fit_kernel_ms > 0.0 ? wait_ms / sum.last_fit_kernel_ms : 0.0;
+  return YTM_OK;
+}
+
+namespace {
+int fit_range(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t count, const uint32_t* drop,
+              const float* inject) {
   ++m->planes_version;  // before any launch: also when the fit fails part-way
   m->stats.last_fit_samples = 0;
   m->stats.last_fit_updates = 0;
@@ -764,11 +825,11 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   int rng_slots = 0;
   size_t lds = 0;
   // The streaming kernel pays when few samples need feedback: it is taken unless the last
-  // fit had feedback at half of its samples or more (config 1: at nearly every sample, where
-  // the resident kernel is 11% faster), or YTM_TRAIN_STREAM forces it (1) or rules it out (0).
+  // fit had feedback at kStreamBelow of its samples or more, or YTM_TRAIN_STREAM forces it
+  // (1) or rules it out (0).
   const char* stream_env = std::getenv("YTM_TRAIN_STREAM");
   const bool stream_forced = stream_env && std::atoi(stream_env) > 0;
-  if ((stream_forced || m->feedback_frac < 0.5) && stream_geometry(m, inj, global, count, &g)) {
+  if ((stream_forced || m->feedback_frac < kStreamBelow) && stream_geometry(m, inj, global, count, &g)) {
     kind = ytm::TrainKind::kStream;
     cpw = ytm::kStreamClauses;
     lds = ytm::stream_lds_bytes(g, g.threads);
@@ -930,6 +991,7 @@ int ytm_fit_dataset(ytm_model* m, const ytm_dataset* ds, int64_t first, int64_t 
   m->stats.last_fit_launches = launches;
   return finish(YTM_OK);
 }
+}  // namespace
 
 int ytm_fit(ytm_model* m, const uint32_t* encX, const int32_t* encY, int64_t N, const uint32_t* drop,
             const float* inject) {
