@@ -308,7 +308,7 @@ def run_config(cfg: int, warmup: int, steps: int, cpu: bool, n_train=None, n_tes
         log(f"[bench] config {cfg} epoch {e + 1}{' (timed)' if e >= warmup else ''}: wall {wall:.3f}s "
             f"kernel {ep['kernel_ms']:.1f}ms updates {ep['updates']} ({ep['updates'] / N:.2f}/sample) "
             f"feedback samples {ep['feedback']} evaluations {ep['evals']} workgroups {ep['wgs']} "
-            f"kernel {KIND_NAMES.get(ep['kind'], ep['kind'])} wait {ep['wait']:.3f}")
+            f"kernel {KIND_NAMES.get(ep['kind'], ep['kind'])} wait {ep['wait']:.3f} launches {ep['launches']}")
         if os.environ.get("YTM_TRAIN_PROFILE") == "4":
             d = st["last_fit_draws"]
             log(f"[bench]   counter-stream words per sample (lane draw sites): reservoir {d[0] / N:.0f} "
