@@ -2804,14 +2804,18 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           int kk = 0;
           const bool small_w = lds_load(&s_wmax) < 512;
           if (g.vote_table && small_w) {
-            // lane k < K: its class's vote from the 16 nibbles of the selection mask
+            // lane k < K: its class's vote from the 16 nibbles of the selection mask.  Every
+            // lane reads (lanes >= K an entry of class 0), through a 32-bit LDS address, so
+            // that the 16 reads go out together with no change of the exec mask.
+            typedef const __attribute__((address_space(3))) short* LdsShorts;
+            const LdsShorts vt_lane = (LdsShorts)(s_vt + (lane < K ? lane : 0));
+            int e[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) e[j] = (int)vt_lane[(j * 16 + (int)((smask >> (4 * j)) & 15ull)) * K];
             int acc = 0;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-              const int v = (int)((smask >> (4 * j)) & 15ull);
-              acc += lane < K ? (int)s_vt[(j * 16 + v) * K + lane] : 0;
-            }
-            mine = acc;
+            for (int j = 0; j < 16; ++j) acc += e[j];
+            mine = lane < K ? acc : 0;
             kk = K;
           } else if (small_w) {
             const int nbias = 512 * __popcll(smask);
