@@ -467,6 +467,36 @@ def test_scoring_lists_follow_the_state():
     data.release()
 
 
+@pytest.mark.parametrize("wmax", [2048, 2049, 100000])
+def test_wide_scoring_weight_range(wmax):
+    """One-patch wide scoring with 4 or more classes sums the votes of a wave's 64 clauses
+    on the matrix cores while every weight of those clauses is at most 2048 in magnitude
+    (f16 holds it exactly) and adds them one by one otherwise: random states with weights
+    up to +-2048 (both bounds present), one weight of 2049 in the second wave's clauses,
+    and weights up to +-100000, against the oracle."""
+    print(f"[wide weights] wmax {wmax}", flush=True)
+    rng = np.random.default_rng(31)
+    kw = dict(number_of_clauses_per_class=300, T=50, s=5.0, dim=(28, 28, 1), n_classes=10)
+    tm = MultiClassTM(**kw, seed=7)
+    C, L, K = tm.number_of_clauses, tm.number_of_literals, tm.number_of_outputs
+    ta = np.where(rng.random((C, L)) < 3.0 / L, 200, 60).astype(np.uint32)
+    lim = min(wmax, 2048) if wmax != 100000 else wmax
+    w = rng.integers(-lim, lim + 1, (C, K)).astype(np.float32)
+    w[0, :], w[1, :] = 2048.0, -2048.0
+    if wmax == 2049:
+        w[100, 3] = 2049.0
+    tm.load_state_dict({"state": {"ta_state": ta, "clause_weights": w,
+                                  "patch_weights": np.zeros((C, 1), np.int32), "min_y": None, "max_y": None}})
+    Xt = (rng.random((700, 28 * 28)) < 0.5).astype(np.uint32)
+    encXt = tm.encode(Xt)
+    oracle = orc.OracleTM(300, 50, 5.0, (28, 28, 1), 10)
+    oracle.load_state(tm.get_ta_state(), tm.get_weights(), tm.get_patch_weights(), tm.stats()["step"])
+    want = oracle.score(encXt)
+    assert np.count_nonzero(want) > want.size // 2, "a meaningful comparison needs firing clauses"
+    np.testing.assert_array_equal(tm.score(encXt, is_X_encoded=True), want)
+    tm.release()
+
+
 def test_fit_conv_lists_of_literal_indices():
     """Literal lists hold byte offsets into the literal-major sample only while those fit 16
     bits; with 696 literals over 29 patch words ((L-1) * 4 * 29 > 65535) they hold literal

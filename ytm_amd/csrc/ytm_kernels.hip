@@ -941,7 +941,9 @@ hipError_t launch_fill_u64(unsigned long long* p, int64_t n, hipStream_t s) {
 constexpr int kWideTile = 32;
 constexpr int64_t kWideLdsBytes = 96 * 1024;
 
-template <bool OUT>
+// MMA: class votes on the matrix cores (K >= 4; fewer classes keep the LDS atomics, and
+// their kernel the registers of that path alone).
+template <bool OUT, bool MMA = false>
 __global__ __launch_bounds__(1024) void wide_kernel(const uint32_t* __restrict__ planes,
                                                     const uint16_t* __restrict__ lists,
                                                     const int32_t* __restrict__ nlit, const float* __restrict__ w,
@@ -949,6 +951,7 @@ __global__ __launch_bounds__(1024) void wide_kernel(const uint32_t* __restrict__
                                                     long long* __restrict__ acc, uint32_t* __restrict__ out) {
   extern __shared__ uint32_t s_xw[];  // [W * 32]: word l = literal l over the tile's samples
   __shared__ long long s_sum[kWideTile * kTileMaxK];
+  __shared__ __attribute__((aligned(16))) uint32_t s_fw[MMA ? 16 * kWave : 1];  // each wave's fire masks
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave, nwv = blockDim.x / kWave;
   const int sl = lane & 31, half = lane >> 5;  // transpose: sample sl of word 2 * pair + half
@@ -991,11 +994,59 @@ __global__ __launch_bounds__(1024) void wide_kernel(const uint32_t* __restrict__
                   s_xw[q.z & 0xFFFFu] & s_xw[q.z >> 16] & s_xw[q.w & 0xFFFFu] & s_xw[q.w >> 16];
         }
       }
-      if (!OUT && fire) {
-        for (int k = 0; k < (int)g.K; ++k) {
-          const long long v = (long long)w[c * g.K + k];
-          for (uint32_t f = fire; f; f &= f - 1u)
-            atomicAdd((unsigned long long*)&s_sum[(__ffs((int)f) - 1) * g.K + k], (unsigned long long)v);
+      if (!OUT) {
+        // The wave's votes as one product on the matrix cores: sums[sample][k] = sum over
+        // its 64 clauses of fire[sample][clause] * w[clause][k], eight clauses per
+        // v_mfma_f32_32x32x8f16 (A: lane l row l % 32 = sample, B: lane l column l % 32 =
+        // class, both with clauses 4 * (l / 32) + 0..3 of the step; D: lane l column
+        // l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4).  Weights are integer-valued
+        // (ytm_set_weights refuses others; training moves them by 1), so the product is exact
+        // while every weight of the wave is at most 2048 in magnitude (f16 holds it, and
+        // 64 * 2048 < 2^24 keeps the f32 sums exact); otherwise the firing samples' weights
+        // go in one by one.
+        const int K = (int)g.K;
+        bool lane_ok = MMA;  // every weight this lane loads is within 2048
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        typedef float float16_t __attribute__((ext_vector_type(16)));
+        float16_t d;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) d[r] = 0.0f;
+        const int col = lane & 31, kq = 4 * (lane >> 5);
+        if (MMA) {
+          s_fw[wave * kWave + lane] = fire;
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll 2
+          for (int st = 0; st < kWave / 8; ++st) {
+            const uint4 f4 = *(const uint4*)&s_fw[wave * kWave + 8 * st + kq];
+            half4_t av, bv;
+            av[0] = (_Float16)(float)((f4.x >> col) & 1u);
+            av[1] = (_Float16)(float)((f4.y >> col) & 1u);
+            av[2] = (_Float16)(float)((f4.z >> col) & 1u);
+            av[3] = (_Float16)(float)((f4.w >> col) & 1u);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int64_t cc = c0 + 8 * st + kq + j;
+              const float wf = cc < ce && col < K ? w[cc * g.K + col] : 0.0f;
+              lane_ok = lane_ok && fabsf(wf) <= 2048.0f;
+              bv[j] = (_Float16)wf;
+            }
+            d = __builtin_amdgcn_mfma_f32_32x32x8f16(av, bv, d, 0, 0, 0);
+          }
+        }
+        if (__all(lane_ok)) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = 8 * (r >> 2) + kq + (r & 3);
+            if (col < K && row < ns && d[r] != 0.0f)
+              atomicAdd((unsigned long long*)&s_sum[row * g.K + col], (unsigned long long)(long long)d[r]);
+          }
+        } else if (fire) {
+          for (int k = 0; k < K; ++k) {
+            const long long v = (long long)w[c * g.K + k];
+            for (uint32_t f = fire; f; f &= f - 1u)
+              atomicAdd((unsigned long long*)&s_sum[(__ffs((int)f) - 1) * g.K + k], (unsigned long long)v);
+          }
         }
       }
       unsigned long long over = __ballot(n > kScoreListCap);
@@ -1136,7 +1187,10 @@ hipError_t launch_score_wide(const uint32_t* planes, const float* w, const uint3
   // waves, 2.0M -> 1.05M).
   const size_t lds = (size_t)(g.W * 32) * 4;
   const int threads = lds <= 64 * 1024 ? 512 : 1024;
-  wide_kernel<false><<<grid, threads, lds, s>>>(planes, lists, nlit, w, X, N, g, nch > 0 ? nch : 1, acc, nullptr);
+  if (g.K >= 4)  // votes on the matrix cores: config 2 inference 187M -> 234M samples/s in the kernel
+    wide_kernel<false, true><<<grid, threads, lds, s>>>(planes, lists, nlit, w, X, N, g, nch > 0 ? nch : 1, acc, nullptr);
+  else
+    wide_kernel<false><<<grid, threads, lds, s>>>(planes, lists, nlit, w, X, N, g, nch > 0 ? nch : 1, acc, nullptr);
   return hipGetLastError();
 }
 
