@@ -2737,17 +2737,24 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
     } else {
       // ---- evaluation: claim samples in order, evaluate with the current state, publish
       const bool own = lane < n_own;
+      // per phase (drop flags never change, include counts only at stops): the lanes whose
+      // clause takes part, and those whose clause is empty (an empty clause fires in training)
+      const bool live = own && s_drop[lane] == 0;
+      const bool empty = s_ninc[lane] == 0;
       for (;;) {
-        if (lds_load(&ctl.stop) >= 0) break;
+        // the stop flag, a claim and the consumer's position in one LDS round trip
+        const int stop_now = __hip_atomic_load(&ctl.stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         int s = 0;
         if (lane == 0) s = atomicAdd(&ctl.claim, 1);
+        int cons = lds_load(&ctl.consume);
+        if (stop_now >= 0) break;
         s = lane_value(s, 0);
         if (s >= a.N) break;
         // at most min(D, depth0 + consumed samples of this phase) ahead of the consumer
         bool skip = false;
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         for (unsigned spins = 1;; ++spins) {
-          const int cons = lds_load(&ctl.consume);
+          if (spins > 1) cons = lds_load(&ctl.consume);
           const int ahead = depth0 + (cons - next) < D ? depth0 + (cons - next) : D;
           if (s < cons + ahead) break;
           if (lds_load(&ctl.stop) >= 0) {  // stopped before s: s is past the stop sample
@@ -2785,7 +2792,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           const uint4 mv = s_maskT[w4 * kStreamClauses + lane], xv = nx4[w4];
           bad |= (mv.x & xv.x) | (mv.y & xv.y) | (mv.z & xv.z) | (mv.w & xv.w);
         }
-        const bool fire = own && s_drop[lane] == 0 && (s_ninc[lane] == 0 || bad == 0u);
+        const bool fire = live && (empty || bad == 0u);
         // a stop set meanwhile lies before s: its row will not be read
         if (lds_load(&ctl.stop) >= 0) break;
         // select_active (kernel.cu:285-316) with one patch: selected when the rank-1 draw is
