@@ -2741,6 +2741,13 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       // clause takes part, and those whose clause is empty (an empty clause fires in training)
       const bool live = own && s_drop[lane] == 0;
       const bool empty = s_ninc[lane] == 0;
+      // the last sample published before this phase (rows past the stop, repaired): later
+      // samples need no look at the ring's publish marks
+      int pub_hi = -1;
+      {
+        const int ps = lane < D ? s_pub[lane] : -1;
+        pub_hi = wave_max_i32(ps);
+      }
       for (;;) {
         // the stop flag, a claim and the consumer's position in one LDS round trip
         const int stop_now = __hip_atomic_load(&ctl.stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -2776,7 +2783,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           __builtin_amdgcn_s_sleep(1);
         }
         if (skip) break;
-        if (s_pub[s & (D - 1)] == s) continue;  // published before the last stop, and repaired
+        if (s <= pub_hi && s_pub[s & (D - 1)] == s) continue;  // published before the last stop, and repaired
         // the sample's complemented words (broadcast reads below; kept in the sample's ring
         // slot for the repairs after a stop) and its targets
         uint32_t* nx = s_nx + (int64_t)(s & (D - 1)) * Wp;
