@@ -2787,8 +2787,11 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         // the sample's complemented words (broadcast reads below; kept in the sample's ring
         // slot for the repairs after a stop) and its targets
         uint32_t* nx = s_nx + (int64_t)(s & (D - 1)) * Wp;
+        // the targets' load first (every lane reads a valid entry), so that it is in flight
+        // together with the words' instead of after them
+        const int32_t yv = a.Y[(int64_t)s * K + (lane < K ? lane : 0)];
         for (int64_t w = lane; w < g.W; w += kWave) nx[w] = ~a.X[(int64_t)s * g.W + w];
-        if (lane < K) s_yring[(s & (D - 1)) * K + lane] = a.Y[(int64_t)s * K + lane];
+        if (lane < K) s_yring[(s & (D - 1)) * K + lane] = yv;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         // fast_eval (kernel.cu:255-282): an empty clause fires in training
