@@ -2714,16 +2714,25 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         // feedback possible in row q?  prob > 0 for some class (class_fb, kernel.cu:508-529)
         const bool live = here && q < ncomp;
         const long long S = (long long)(v - (units << 44)) + bias_k;
+        // the selections of the complete rows, lane r holding row j + r's, read together with
+        // the targets (instead of one LDS round trip per row below)
+        const unsigned long long ringq = s_ring[(j + (lane < nq ? lane : 0)) & (D - 1)];
+        const int yq = s_yring[((j + (q < nq ? q : 0)) & (D - 1)) * K + k];
         bool fb = false;
         if (live) {
-          const int y = s_yring[((j + q) & (D - 1)) * K + k];
+          const int y = yq;
           fb = class_may_update(g, S, y);  // class_fb(g, S, y).prob > 0
         }
         const unsigned long long fbm = __ballot(fb);
         const int qf = fbm ? (__ffsll((long long)fbm) - 1) / K : ncomp;  // first row with feedback
         // patch weights of the rows before it (select_active, kernel.cu:305), counted in a
         // register of the clause's lane and added to LDS when the phase ends
-        for (int r = 0; r < qf; ++r) pw_add += (int)((s_ring[(j + r) & (D - 1)] >> lane) & 1ull);
+        for (int r = 0; r < qf; ++r) {
+          const unsigned long long rr =
+              ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(ringq >> 32), r) << 32) |
+              (unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)ringq, r);
+          pw_add += (int)((rr >> lane) & 1ull);
+        }
         if (qf < ncomp) {
           if (q == qf) s_S[k] = S;
           stop = j + qf;
