@@ -2766,6 +2766,10 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         if (stop_now >= 0) break;
         s = lane_value(s, 0);
         if (s >= a.N) break;
+        // the sample's targets and (one word per lane) its words, in flight while the
+        // window is checked (every lane reads a valid entry)
+        const int32_t yv = a.Y[(int64_t)s * K + (lane < K ? lane : 0)];
+        const uint32_t xv0 = g.W <= kWave ? a.X[(int64_t)s * g.W + (lane < g.W ? lane : 0)] : 0u;
         // at most min(D, depth0 + consumed samples of this phase) ahead of the consumer
         bool skip = false;
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -2796,10 +2800,11 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         // the sample's complemented words (broadcast reads below; kept in the sample's ring
         // slot for the repairs after a stop) and its targets
         uint32_t* nx = s_nx + (int64_t)(s & (D - 1)) * Wp;
-        // the targets' load first (every lane reads a valid entry), so that it is in flight
-        // together with the words' instead of after them
-        const int32_t yv = a.Y[(int64_t)s * K + (lane < K ? lane : 0)];
-        for (int64_t w = lane; w < g.W; w += kWave) nx[w] = ~a.X[(int64_t)s * g.W + w];
+        if (g.W <= kWave) {
+          if (lane < g.W) nx[lane] = ~xv0;
+        } else {
+          for (int64_t w = lane; w < g.W; w += kWave) nx[w] = ~a.X[(int64_t)s * g.W + w];
+        }
         if (lane < K) s_yring[(s & (D - 1)) * K + lane] = yv;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
