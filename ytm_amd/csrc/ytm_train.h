@@ -2986,6 +2986,8 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
       // row published from here on carries kgen + 1 units at once.
       ++kgen;
       __syncthreads();  // include counts of the updated clauses
+      // the updated clauses, lane tk holding task tk's (read once for all the rows)
+      const int tidx = lane < ntask ? s_task_idx[lane] : 0;
       // in row order from the next row, which the consumer waits for first
       for (int u = wave; u < D; u += nwv) {
         const int q = (next + u) & (D - 1);
@@ -2999,7 +3001,8 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
           const int64_t w = w0 + lane;
           const uint32_t nxw = w < g.W ? nxr[w] : 0u;
           for (int tk = 0; tk < ntask; ++tk) {
-            const uint32_t mw = w < g.W ? s_planes[s_task_idx[tk] * cw + (int64_t)(g.np - 1) * g.W + w] : 0u;
+            const int tix = __builtin_amdgcn_readlane(tidx, tk);
+            const uint32_t mw = w < g.W ? s_planes[tix * cw + (int64_t)(g.np - 1) * g.W + w] : 0u;
             if (__any((mw & nxw) != 0u)) badm |= 1ull << tk;
           }
         }
@@ -3007,7 +3010,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         // draw of select_active, as in the evaluation above)
         bool nsel = false;
         if (lane < ntask) {
-          const int idx = s_task_idx[lane];
+          const int idx = tidx;
           if (s_ninc[idx] == 0 || ((badm >> lane) & 1ull) == 0ull)
             nsel = uniform_from_word(
                        counted_site(a, a.step0 + (uint64_t)r, (uint32_t)(c_begin + idx), TAG_SEL, 0u).x) < 1.0f;
@@ -3015,7 +3018,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         const unsigned long long nb = __ballot(nsel);
         unsigned long long chg = 0ull, nsm = 0ull;
         for (int tk = 0; tk < ntask; ++tk) {
-          const int idx = s_task_idx[tk];
+          const int idx = __builtin_amdgcn_readlane(tidx, tk);
           chg |= 1ull << idx;
           nsm |= ((nb >> tk) & 1ull) << idx;
         }
@@ -3023,7 +3026,7 @@ __device__ __forceinline__ void train_stream_body(const TrainArgs& a, const Geom
         if (lane < K) {
           long long delta = 0;
           for (int tk = 0; tk < ntask; ++tk) {
-            const int idx = s_task_idx[tk];
+            const int idx = __builtin_amdgcn_readlane(tidx, tk);
             if ((nsm >> idx) & 1ull) delta += s_wt[lane * kStreamClauses + idx];
             if ((om >> idx) & 1ull) delta -= s_wt_old[lane * kStreamClauses + idx];
           }
